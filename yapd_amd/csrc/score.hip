@@ -1,0 +1,358 @@
+// (c) CFG combine + prior-calibrated PMI + time-shifted-quantile unmask.
+//
+// One 256-thread workgroup per (pair, position) streams the cond and null
+// logit rows once from HBM (dword loads; rows are only 4-byte aligned since
+// V = 8194), keeping an online (max, sum-exp) per branch and the argmax of
+// the guided score.  The guided argmax uses (1+w)*lc - w*lu, which differs
+// from the reference's lsc + w*(lsc - lsu) (server/engine.py:536-539) only by
+// a per-row constant.  A second, tiny kernel (one wave per pair) then runs the
+// per-pair decision rule of server/engine.py:563-593: ranks by pairwise
+// comparison, the linear quantile with the reference's fp32 op order, top-n
+// unmask.  Two launches instead of a "last workgroup finishes the pair"
+// handoff: on a multi-XCD part each agent-scope release/acquire fence writes
+// back / invalidates the XCD's L2, which costs far more than a launch.
+#include <cmath>
+
+#include "common.h"
+
+namespace yapd {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;  // dwords per row per thread per iteration
+
+struct ScoreParams {
+  const uint16_t* logits;
+  int64_t seq_stride, pos_stride;
+  int n_pairs, bl, vocab, cond_row0, pair_row_step, has_uncond, null_row_offset;
+  const float* log_prior;
+  const int64_t* xt_in;
+  const int64_t* k_step;
+  const uint8_t* active;
+  const int32_t* sched;
+  const float* q_tab;
+  int K;
+  float cfg_w, cfg_w1;  // w and (float)(1 + w)
+  int quantile_on;
+  int64_t mask_id, stop_id;
+  float temperature;
+  int pos_gumbel;
+  uint64_t seed, rng_offset;
+  int64_t* sampled;
+  float* pmi;
+  uint8_t* unmask;
+  int64_t* xt_out;
+  int32_t* n_mask_after;
+  uint8_t* hit_eos;
+};
+
+// Philox4x32-10 (Salmon et al., SC'11).
+__device__ __forceinline__ u32x4_t philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                                 uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = static_cast<uint64_t>(0xD2511F53u) * c0;
+    const uint64_t p1 = static_cast<uint64_t>(0xCD9E8D57u) * c2;
+    const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c3 ^ k1;
+    c1 = static_cast<uint32_t>(p1);
+    c3 = static_cast<uint32_t>(p0);
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return u32x4_t{c0, c1, c2, c3};
+}
+
+__device__ __forceinline__ float gumbel_from_u32(uint32_t x) {
+  const float u = (static_cast<float>(x >> 9) + 0.5f) * 0x1p-23f;  // in (0, 1), exact
+  return -logf(-logf(u));
+}
+
+struct RowStats {
+  float m, s;
+};
+
+__device__ __forceinline__ RowStats merge_stats(RowStats a, RowStats b) {
+  const float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return {m, 0.f};
+  const float sa = a.m == -INFINITY ? 0.f : a.s * __expf(a.m - m);
+  const float sb = b.m == -INFINITY ? 0.f : b.s * __expf(b.m - m);
+  return {m, sa + sb};
+}
+
+struct Best {
+  float g;
+  int idx;
+  float lc, lu;
+};
+
+__device__ __forceinline__ bool better(const Best& o, const Best& cur) {
+  return o.g > cur.g || (o.g == cur.g && o.idx < cur.idx);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams P) {
+  const int item = blockIdx.x;
+  const int pair = item / P.bl;
+  const int pos = item - pair * P.bl;
+  const int tid = threadIdx.x;
+  const int64_t crow = static_cast<int64_t>(P.cond_row0) + static_cast<int64_t>(pair) * P.pair_row_step;
+  const uint16_t* rc = P.logits + crow * P.seq_stride + static_cast<int64_t>(pos) * P.pos_stride;
+  const uint16_t* ru = rc + static_cast<int64_t>(P.null_row_offset) * P.seq_stride;
+  const uint32_t* wc = reinterpret_cast<const uint32_t*>(rc);
+  const uint32_t* wu = reinterpret_cast<const uint32_t*>(ru);
+  const bool has_u = P.has_uncond != 0;
+  const int V = P.vocab;
+  const int nw = V >> 1;
+  const float w = P.cfg_w, w1 = P.cfg_w1;
+  const bool sample = P.temperature > 0.f;
+  const uint32_t key0 = static_cast<uint32_t>(P.seed), key1 = static_cast<uint32_t>(P.seed >> 32);
+  const uint32_t off0 = static_cast<uint32_t>(P.rng_offset), off1 = static_cast<uint32_t>(P.rng_offset >> 32);
+
+  RowStats sc{-INFINITY, 0.f}, su{-INFINITY, 0.f};
+  Best best{-INFINITY, 0x7fffffff, 0.f, 0.f};
+
+  auto consider = [&](int v, float lc, float lu, float noise) {
+    float g = has_u ? __fsub_rn(__fmul_rn(w1, lc), __fmul_rn(w, lu)) : lc;
+    if (sample) g = __fadd_rn(g, __fmul_rn(P.temperature, noise));
+    if (g > best.g) best = Best{g, v, lc, lu};
+  };
+
+  for (int base = 0; base < nw; base += kThreads * kUnroll) {
+    uint32_t xc[kUnroll], xu[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int j = base + u * kThreads + tid;
+      xc[u] = j < nw ? __builtin_nontemporal_load(wc + j) : 0xff80ff80u;
+      xu[u] = (has_u && j < nw) ? __builtin_nontemporal_load(wu + j) : 0xff80ff80u;
+    }
+    float cmc = -INFINITY, cmu = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      cmc = fmaxf(cmc, fmaxf(bf16lo(xc[u]), bf16hi(xc[u])));
+      cmu = fmaxf(cmu, fmaxf(bf16lo(xu[u]), bf16hi(xu[u])));
+    }
+    if (cmc != -INFINITY) {
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc += __expf(bf16lo(xc[u]) - cmc) + __expf(bf16hi(xc[u]) - cmc);
+      sc = merge_stats(sc, RowStats{cmc, acc});
+    }
+    if (has_u && cmu != -INFINITY) {
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc += __expf(bf16lo(xu[u]) - cmu) + __expf(bf16hi(xu[u]) - cmu);
+      su = merge_stats(su, RowStats{cmu, acc});
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int j = base + u * kThreads + tid;
+      if (j < nw) {
+        float n0 = 0.f, n1 = 0.f;
+        if (sample) {
+          const u32x4_t r = philox4x32_10(static_cast<uint32_t>(j >> 1), static_cast<uint32_t>(item), off0, off1,
+                                          key0, key1);
+          n0 = gumbel_from_u32((j & 1) ? r.z : r.x);
+          n1 = gumbel_from_u32((j & 1) ? r.w : r.y);
+        }
+        consider(2 * j, bf16lo(xc[u]), bf16lo(xu[u]), n0);
+        consider(2 * j + 1, bf16hi(xc[u]), bf16hi(xu[u]), n1);
+      }
+    }
+  }
+  if ((V & 1) && tid == 0) {  // odd vocab: the last element sits alone
+    const float lc = bf16_to_f32(rc[V - 1]);
+    const float lu = has_u ? bf16_to_f32(ru[V - 1]) : 0.f;
+    sc = merge_stats(sc, RowStats{lc, 1.f});
+    if (has_u) su = merge_stats(su, RowStats{lu, 1.f});
+    float n = 0.f;
+    if (sample) {
+      const u32x4_t r = philox4x32_10(static_cast<uint32_t>((V - 1) >> 2), static_cast<uint32_t>(item), off0, off1,
+                                      key0, key1);
+      const int sel = (V - 1) & 3;
+      n = gumbel_from_u32(sel == 0 ? r.x : sel == 1 ? r.y : sel == 2 ? r.z : r.w);
+    }
+    consider(V - 1, lc, lu, n);
+  }
+
+  // Wave reduction, then across the four waves through LDS.
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    sc = merge_stats(sc, RowStats{shfl_xor_f(sc.m, m), shfl_xor_f(sc.s, m)});
+    su = merge_stats(su, RowStats{shfl_xor_f(su.m, m), shfl_xor_f(su.s, m)});
+    const Best o{shfl_xor_f(best.g, m), shfl_xor_i(best.idx, m), shfl_xor_f(best.lc, m), shfl_xor_f(best.lu, m)};
+    if (better(o, best)) best = o;
+  }
+  __shared__ float s_f[kThreads / 64][7];
+  __shared__ int s_i[kThreads / 64];
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
+    s_f[wave][0] = sc.m;
+    s_f[wave][1] = sc.s;
+    s_f[wave][2] = su.m;
+    s_f[wave][3] = su.s;
+    s_f[wave][4] = best.g;
+    s_f[wave][5] = best.lc;
+    s_f[wave][6] = best.lu;
+    s_i[wave] = best.idx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int q = 1; q < kThreads / 64; ++q) {
+      sc = merge_stats(sc, RowStats{s_f[q][0], s_f[q][1]});
+      su = merge_stats(su, RowStats{s_f[q][2], s_f[q][3]});
+      const Best o{s_f[q][4], s_i[q], s_f[q][5], s_f[q][6]};
+      if (better(o, best)) best = o;
+    }
+    const int x = best.idx;
+    const float lpr = P.log_prior[x];
+    // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
+    float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(best.lc - sc.m), sc.s), 1e-8f)), lpr);
+    if (has_u) {
+      const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(best.lu - su.m), su.s), 1e-8f)), lpr);
+      pmi = __fsub_rn(__fmul_rn(w1, pmi), __fmul_rn(w, pmi_u));
+    }
+    if (P.pos_gumbel) {
+      const int64_t xt = P.xt_in[item];
+      if (xt == P.mask_id) {
+        const u32x4_t r = philox4x32_10(0xffffffffu, static_cast<uint32_t>(item), off0, off1, key0, key1);
+        pmi = __fadd_rn(pmi, gumbel_from_u32(r.x));
+      }
+    }
+    P.sampled[item] = x;
+    P.pmi[item] = pmi;
+  }
+}
+
+// One wave per pair: the decision rule of server/engine.py:563-593.
+__global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParams P) {
+  const int pair = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (pair >= P.n_pairs) return;
+  const int bl = P.bl;
+  const int lane = threadIdx.x & 63;
+  const int64_t ib = static_cast<int64_t>(pair) * bl;
+  const bool valid = lane < bl;
+  const int64_t xt = valid ? P.xt_in[ib + lane] : 0;
+  const float key = valid ? P.pmi[ib + lane] : 0.f;
+  const int64_t smp = valid ? P.sampled[ib + lane] : 0;
+  const bool msk = valid && xt == P.mask_id;
+  const uint64_t bal = __ballot(msk);
+  const int m = __popcll(bal);
+
+  int asc = 0, desc = 0;
+  for (int j = 0; j < bl; ++j) {
+    if ((bal >> j) & 1ull) {
+      const float pj = readlane_f(key, j);
+      asc += (pj < key) || (pj == key && j < lane);
+      desc += (pj > key) || (pj == key && j < lane);
+    }
+  }
+  const int64_t k = P.k_step[pair];
+  int kc = k < P.K - 1 ? static_cast<int>(k) : P.K - 1;
+  kc = kc < 0 ? 0 : kc;
+  // p = q_t[k] * (m-1).clamp_min(0).float(); lo/hi = floor/ceil; linear interpolation.
+  const float p = __fmul_rn(P.q_tab[kc], static_cast<float>(m > 1 ? m - 1 : 0));
+  int lo = static_cast<int>(floorf(p));
+  int hi = static_cast<int>(ceilf(p));
+  lo = lo < 0 ? 0 : lo;
+  hi = hi < 0 ? 0 : hi;
+  const uint64_t blo = __ballot(msk && asc == lo);
+  const uint64_t bhi = __ballot(msk && asc == hi);
+  const float v_lo = blo ? readlane_f(key, __ffsll(static_cast<unsigned long long>(blo)) - 1) : INFINITY;
+  const float v_hi = bhi ? readlane_f(key, __ffsll(static_cast<unsigned long long>(bhi)) - 1) : INFINITY;
+  const float tau = __fadd_rn(v_lo, __fmul_rn(__fsub_rn(p, static_cast<float>(lo)), __fsub_rn(v_hi, v_lo)));
+  const int n_quant = P.quantile_on ? __popcll(__ballot(msk && key >= tau)) : 0;
+  const int n_sched = min(P.sched[kc], m);
+  int n = min(max(n_sched, n_quant), m);
+  if (k >= P.K - 1) n = m;
+  if (m == 0) n = 0;
+  const bool act = P.active == nullptr || P.active[pair] != 0;
+  const bool unm = act && msk && desc < n;
+  const int64_t xo = unm ? smp : xt;
+  if (valid) {
+    P.unmask[ib + lane] = unm ? 1 : 0;
+    P.xt_out[ib + lane] = xo;
+  }
+  const int n_after = __popcll(__ballot(valid && xo == P.mask_id));
+  const bool eos = __ballot(valid && xo == P.stop_id) != 0ull;
+  if (lane == 0) {
+    P.n_mask_after[pair] = n_after;
+    P.hit_eos[pair] = eos ? 1 : 0;
+  }
+}
+
+}  // namespace
+}  // namespace yapd
+
+extern "C" int yapd_score_cfg_pmi_unmask(
+    const void* logits, int64_t seq_stride, int64_t pos_stride, int n_pairs, int bl, int vocab, int cond_row0,
+    int pair_row_step, int has_uncond, int null_row_offset, const float* log_prior, const int64_t* xt_in,
+    const int64_t* k_step, const uint8_t* active, const int32_t* sched, const float* q_tab, int K, float cfg_w,
+    int quantile_on, int64_t mask_id, int64_t stop_id, float temperature, int pos_gumbel, uint64_t seed,
+    uint64_t rng_offset, int64_t* sampled_out, float* pmi_out, uint8_t* unmask_out, int64_t* xt_out,
+    int32_t* n_mask_after_out, uint8_t* hit_eos_out, void* stream) {
+  YAPD_REQUIRE(logits != nullptr, "score: logits is NULL");
+  YAPD_REQUIRE((reinterpret_cast<uintptr_t>(logits) & 3u) == 0, "score: logits must be 4-byte aligned");
+  YAPD_REQUIRE(n_pairs >= 1 && bl >= 1 && bl <= 64, "score: need n_pairs >= 1 and 1 <= bl <= 64 (got %d, %d)",
+               n_pairs, bl);
+  YAPD_REQUIRE(vocab >= 1, "score: vocab must be >= 1 (got %d)", vocab);
+  YAPD_REQUIRE(static_cast<int64_t>(n_pairs) * bl < (int64_t{1} << 31), "score: too many items");
+  YAPD_REQUIRE(seq_stride % 2 == 0 && pos_stride % 2 == 0, "score: strides must be even (got %lld, %lld)",
+               static_cast<long long>(seq_stride), static_cast<long long>(pos_stride));
+  YAPD_REQUIRE(pos_stride >= vocab, "score: pos_stride %lld < vocab %d", static_cast<long long>(pos_stride), vocab);
+  YAPD_REQUIRE(cond_row0 >= 0 && pair_row_step >= 0, "score: negative row layout");
+  YAPD_REQUIRE(K >= 1, "score: K must be >= 1");
+  YAPD_REQUIRE(temperature >= 0.f, "score: temperature must be >= 0");
+  YAPD_REQUIRE(log_prior && xt_in && k_step && sched && q_tab, "score: NULL input pointer");
+  YAPD_REQUIRE(sampled_out && pmi_out && unmask_out && xt_out && n_mask_after_out && hit_eos_out,
+               "score: NULL output pointer");
+  yapd::ScoreParams P;
+  P.logits = static_cast<const uint16_t*>(logits);
+  P.seq_stride = seq_stride;
+  P.pos_stride = pos_stride;
+  P.n_pairs = n_pairs;
+  P.bl = bl;
+  P.vocab = vocab;
+  P.cond_row0 = cond_row0;
+  P.pair_row_step = pair_row_step;
+  P.has_uncond = has_uncond;
+  P.null_row_offset = has_uncond ? null_row_offset : 0;
+  P.log_prior = log_prior;
+  P.xt_in = xt_in;
+  P.k_step = k_step;
+  P.active = active;
+  P.sched = sched;
+  P.q_tab = q_tab;
+  P.K = K;
+  P.cfg_w = cfg_w;
+  P.cfg_w1 = static_cast<float>(1.0 + static_cast<double>(cfg_w));
+  P.quantile_on = quantile_on;
+  P.mask_id = mask_id;
+  P.stop_id = stop_id;
+  P.temperature = temperature;
+  P.pos_gumbel = pos_gumbel;
+  P.seed = seed;
+  P.rng_offset = rng_offset;
+  P.sampled = sampled_out;
+  P.pmi = pmi_out;
+  P.unmask = unmask_out;
+  P.xt_out = xt_out;
+  P.n_mask_after = n_mask_after_out;
+  P.hit_eos = hit_eos_out;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(yapd::score_items_kernel, dim3(n_pairs * bl), dim3(yapd::kThreads), 0, st, P);
+  YAPD_LAUNCH_CHECK("score_items_kernel launch");
+  const int waves_per_block = yapd::kThreads / 64;
+  hipLaunchKernelGGL(yapd::score_decide_kernel, dim3((n_pairs + waves_per_block - 1) / waves_per_block),
+                     dim3(yapd::kThreads), 0, st, P);
+  YAPD_LAUNCH_CHECK("score_decide_kernel launch");
+  return YAPD_OK;
+}
