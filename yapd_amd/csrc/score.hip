@@ -19,7 +19,7 @@ namespace yapd {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 8;  // dwords per row per thread per iteration
+constexpr int kUnroll = 16;  // dwords per row per thread per full pass (V = 8194: one pass + 1 dword)
 
 struct ScoreParams {
   const uint16_t* logits;
@@ -77,8 +77,9 @@ struct RowStats {
 __device__ __forceinline__ RowStats merge_stats(RowStats a, RowStats b) {
   const float m = fmaxf(a.m, b.m);
   if (m == -INFINITY) return {m, 0.f};
-  const float sa = a.m == -INFINITY ? 0.f : a.s * __expf(a.m - m);
-  const float sb = b.m == -INFINITY ? 0.f : b.s * __expf(b.m - m);
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float sa = a.m == -INFINITY ? 0.f : a.s * __builtin_amdgcn_exp2f((a.m - m) * kLog2e);
+  const float sb = b.m == -INFINITY ? 0.f : b.s * __builtin_amdgcn_exp2f((b.m - m) * kLog2e);
   return {m, sa + sb};
 }
 
@@ -99,6 +100,11 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Streaming pass for one (pair, position).  Per element the VALU work is
+// kept to the minimum the math needs (bf16 unpack, max, one FMA + v_exp and an
+// add per branch, the guided score and a compare/select for the argmax):
+// with 268 MB of logits this kernel sits at the VALU/HBM balance point.
+template <bool kHasU, bool kSample>
 __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams P) {
   const int item = blockIdx.x;
   const int pair = item / P.bl;
@@ -109,89 +115,121 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
   const uint16_t* ru = rc + static_cast<int64_t>(P.null_row_offset) * P.seq_stride;
   const uint32_t* wc = reinterpret_cast<const uint32_t*>(rc);
   const uint32_t* wu = reinterpret_cast<const uint32_t*>(ru);
-  const bool has_u = P.has_uncond != 0;
   const int V = P.vocab;
   const int nw = V >> 1;
   const float w = P.cfg_w, w1 = P.cfg_w1;
-  const bool sample = P.temperature > 0.f;
   const uint32_t key0 = static_cast<uint32_t>(P.seed), key1 = static_cast<uint32_t>(P.seed >> 32);
   const uint32_t off0 = static_cast<uint32_t>(P.rng_offset), off1 = static_cast<uint32_t>(P.rng_offset >> 32);
+  constexpr float kLog2e = 1.4426950408889634f;
 
   RowStats sc{-INFINITY, 0.f}, su{-INFINITY, 0.f};
-  Best best{-INFINITY, 0x7fffffff, 0.f, 0.f};
+  float best_g = -INFINITY;
+  int best_v = 0x7fffffff;
 
-  auto consider = [&](int v, float lc, float lu, float noise) {
-    float g = has_u ? __fsub_rn(__fmul_rn(w1, lc), __fmul_rn(w, lu)) : lc;
-    if (sample) g = __fadd_rn(g, __fmul_rn(P.temperature, noise));
-    if (g > best.g) best = Best{g, v, lc, lu};
+  // Guided score of element v (+ T * Gumbel noise when sampling).
+  auto guided = [&](float lc, float lu, int v) {
+    // one rounding less than (1+w)*lc - w*lu; only ulp-level near-ties can tell
+    float g = kHasU ? __builtin_fmaf(w1, lc, -w * lu) : lc;
+    if (kSample) {
+      const u32x4_t r = philox4x32_10(static_cast<uint32_t>(v >> 2), static_cast<uint32_t>(item), off0, off1,
+                                      key0, key1);
+      const uint32_t word = (v & 3) == 0 ? r.x : (v & 3) == 1 ? r.y : (v & 3) == 2 ? r.z : r.w;
+      g = __fadd_rn(g, __fmul_rn(P.temperature, gumbel_from_u32(word)));
+    }
+    return g;
   };
 
-  for (int base = 0; base < nw; base += kThreads * kUnroll) {
+  // Full passes: every thread owns kUnroll dwords per row, loads issued back to back.
+  int base = 0;
+  for (; base + kThreads * kUnroll <= nw; base += kThreads * kUnroll) {
     uint32_t xc[kUnroll], xu[kUnroll];
+    const uint32_t* pc = wc + base + tid;
+    const uint32_t* pu = wu + base + tid;
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int j = base + u * kThreads + tid;
-      xc[u] = j < nw ? __builtin_nontemporal_load(wc + j) : 0xff80ff80u;
-      xu[u] = (has_u && j < nw) ? __builtin_nontemporal_load(wu + j) : 0xff80ff80u;
+      xc[u] = pc[u * kThreads];
+      if (kHasU) xu[u] = pu[u * kThreads];
     }
-    float cmc = -INFINITY, cmu = -INFINITY;
+    float fc[2 * kUnroll], fu[2 * kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      cmc = fmaxf(cmc, fmaxf(bf16lo(xc[u]), bf16hi(xc[u])));
-      cmu = fmaxf(cmu, fmaxf(bf16lo(xu[u]), bf16hi(xu[u])));
+      fc[2 * u] = bf16lo(xc[u]);
+      fc[2 * u + 1] = bf16hi(xc[u]);
+      if (kHasU) {
+        fu[2 * u] = bf16lo(xu[u]);
+        fu[2 * u + 1] = bf16hi(xu[u]);
+      }
     }
-    if (cmc != -INFINITY) {
-      float acc = 0.f;
+    float mc = fc[0], mu = kHasU ? fu[0] : 0.f;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) acc += __expf(bf16lo(xc[u]) - cmc) + __expf(bf16hi(xc[u]) - cmc);
-      sc = merge_stats(sc, RowStats{cmc, acc});
+    for (int e = 1; e < 2 * kUnroll; ++e) {
+      mc = fmaxf(mc, fc[e]);
+      if (kHasU) mu = fmaxf(mu, fu[e]);
     }
-    if (has_u && cmu != -INFINITY) {
-      float acc = 0.f;
+    const float mcs = mc * kLog2e, mus = mu * kLog2e;
+    float ac = 0.f, au = 0.f;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) acc += __expf(bf16lo(xu[u]) - cmu) + __expf(bf16hi(xu[u]) - cmu);
-      su = merge_stats(su, RowStats{cmu, acc});
+    for (int e = 0; e < 2 * kUnroll; ++e) {
+      ac += __builtin_amdgcn_exp2f(__builtin_fmaf(fc[e], kLog2e, -mcs));
+      if (kHasU) au += __builtin_amdgcn_exp2f(__builtin_fmaf(fu[e], kLog2e, -mus));
     }
+    sc = merge_stats(sc, RowStats{mc, ac});
+    if (kHasU) su = merge_stats(su, RowStats{mu, au});
+    // argmax; the first maximum in index order wins, as torch.argmax does.
+    float pg = -INFINITY;
+    int pe = 0;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = base + u * kThreads + tid;
-      if (j < nw) {
-        float n0 = 0.f, n1 = 0.f;
-        if (sample) {
-          const u32x4_t r = philox4x32_10(static_cast<uint32_t>(j >> 1), static_cast<uint32_t>(item), off0, off1,
-                                          key0, key1);
-          n0 = gumbel_from_u32((j & 1) ? r.z : r.x);
-          n1 = gumbel_from_u32((j & 1) ? r.w : r.y);
-        }
-        consider(2 * j, bf16lo(xc[u]), bf16lo(xu[u]), n0);
-        consider(2 * j + 1, bf16hi(xc[u]), bf16hi(xu[u]), n1);
+    for (int e = 0; e < 2 * kUnroll; ++e) {
+      const float g = guided(fc[e], kHasU ? fu[e] : 0.f, 2 * (base + (e >> 1) * kThreads + tid) + (e & 1));
+      if (g > pg) {
+        pg = g;
+        pe = e;
+      }
+    }
+    if (pg > best_g) {
+      best_g = pg;
+      best_v = 2 * (base + (pe >> 1) * kThreads + tid) + (pe & 1);
+    }
+  }
+  // Tail: the remaining dwords, one per thread at a time.
+  for (int j = base + tid; j < nw; j += kThreads) {
+    const uint32_t xc = wc[j];
+    const uint32_t xu = kHasU ? wu[j] : 0u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float lc = h ? bf16hi(xc) : bf16lo(xc);
+      const float lu = h ? bf16hi(xu) : bf16lo(xu);
+      sc = merge_stats(sc, RowStats{lc, 1.f});
+      if (kHasU) su = merge_stats(su, RowStats{lu, 1.f});
+      const float g = guided(lc, lu, 2 * j + h);
+      if (g > best_g) {
+        best_g = g;
+        best_v = 2 * j + h;
       }
     }
   }
   if ((V & 1) && tid == 0) {  // odd vocab: the last element sits alone
     const float lc = bf16_to_f32(rc[V - 1]);
-    const float lu = has_u ? bf16_to_f32(ru[V - 1]) : 0.f;
+    const float lu = kHasU ? bf16_to_f32(ru[V - 1]) : 0.f;
     sc = merge_stats(sc, RowStats{lc, 1.f});
-    if (has_u) su = merge_stats(su, RowStats{lu, 1.f});
-    float n = 0.f;
-    if (sample) {
-      const u32x4_t r = philox4x32_10(static_cast<uint32_t>((V - 1) >> 2), static_cast<uint32_t>(item), off0, off1,
-                                      key0, key1);
-      const int sel = (V - 1) & 3;
-      n = gumbel_from_u32(sel == 0 ? r.x : sel == 1 ? r.y : sel == 2 ? r.z : r.w);
+    if (kHasU) su = merge_stats(su, RowStats{lu, 1.f});
+    const float g = guided(lc, lu, V - 1);
+    if (g > best_g) {
+      best_g = g;
+      best_v = V - 1;
     }
-    consider(V - 1, lc, lu, n);
   }
+  Best best{best_g, best_v, 0.f, 0.f};
 
   // Wave reduction, then across the four waves through LDS.
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     sc = merge_stats(sc, RowStats{shfl_xor_f(sc.m, m), shfl_xor_f(sc.s, m)});
     su = merge_stats(su, RowStats{shfl_xor_f(su.m, m), shfl_xor_f(su.s, m)});
-    const Best o{shfl_xor_f(best.g, m), shfl_xor_i(best.idx, m), shfl_xor_f(best.lc, m), shfl_xor_f(best.lu, m)};
+    const Best o{shfl_xor_f(best.g, m), shfl_xor_i(best.idx, m), 0.f, 0.f};
     if (better(o, best)) best = o;
   }
-  __shared__ float s_f[kThreads / 64][7];
+  __shared__ float s_f[kThreads / 64][5];
   __shared__ int s_i[kThreads / 64];
   const int wave = tid >> 6;
   if ((tid & 63) == 0) {
@@ -200,8 +238,6 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
     s_f[wave][2] = su.m;
     s_f[wave][3] = su.s;
     s_f[wave][4] = best.g;
-    s_f[wave][5] = best.lc;
-    s_f[wave][6] = best.lu;
     s_i[wave] = best.idx;
   }
   __syncthreads();
@@ -209,15 +245,17 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
     for (int q = 1; q < kThreads / 64; ++q) {
       sc = merge_stats(sc, RowStats{s_f[q][0], s_f[q][1]});
       su = merge_stats(su, RowStats{s_f[q][2], s_f[q][3]});
-      const Best o{s_f[q][4], s_i[q], s_f[q][5], s_f[q][6]};
+      const Best o{s_f[q][4], s_i[q], 0.f, 0.f};
       if (better(o, best)) best = o;
     }
     const int x = best.idx;
     const float lpr = P.log_prior[x];
     // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
-    float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(best.lc - sc.m), sc.s), 1e-8f)), lpr);
-    if (has_u) {
-      const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(best.lu - su.m), su.s), 1e-8f)), lpr);
+    const float lcx = bf16_to_f32(rc[x]);
+    float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lcx - sc.m), sc.s), 1e-8f)), lpr);
+    if (kHasU) {
+      const float lux = bf16_to_f32(ru[x]);
+      const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lux - su.m), su.s), 1e-8f)), lpr);
       pmi = __fsub_rn(__fmul_rn(w1, pmi), __fmul_rn(w, pmi_u));
     }
     if (P.pos_gumbel) {
@@ -348,7 +386,15 @@ extern "C" int yapd_score_cfg_pmi_unmask(
   P.n_mask_after = n_mask_after_out;
   P.hit_eos = hit_eos_out;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(yapd::score_items_kernel, dim3(n_pairs * bl), dim3(yapd::kThreads), 0, st, P);
+  const dim3 grid(n_pairs * bl), block(yapd::kThreads);
+  if (has_uncond && temperature > 0.f)
+    hipLaunchKernelGGL((yapd::score_items_kernel<true, true>), grid, block, 0, st, P);
+  else if (has_uncond)
+    hipLaunchKernelGGL((yapd::score_items_kernel<true, false>), grid, block, 0, st, P);
+  else if (temperature > 0.f)
+    hipLaunchKernelGGL((yapd::score_items_kernel<false, true>), grid, block, 0, st, P);
+  else
+    hipLaunchKernelGGL((yapd::score_items_kernel<false, false>), grid, block, 0, st, P);
   YAPD_LAUNCH_CHECK("score_items_kernel launch");
   const int waves_per_block = yapd::kThreads / 64;
   hipLaunchKernelGGL(yapd::score_decide_kernel, dim3((n_pairs + waves_per_block - 1) / waves_per_block),
