@@ -1,0 +1,457 @@
+// (a) Paged-KV block attention for the block-diffusion step.
+//
+// Every query of a row's current block attends to all kv_len = cache_start +
+// bl keys of that row: the committed prefix plus the whole block,
+// bidirectionally (engines/flashinfer.py:884-886 plans causal=False;
+// engines/torch_sdpa.py:299-307 uses a zero mask).  The block's own K/V are
+// already in the pool (written by the QKV epilogue or yapd_kv_write).
+//
+// Work decomposition: a workgroup of four waves serves one (row, key range)
+// work item for four heads, one head per wave, so a workgroup streams
+// 4 heads x (2 KiB K + 2 KiB V) contiguous bytes per page.  Per 32-key chunk a
+// wave computes S^T = K Q^T (v_mfma_f32_16x16x32_bf16, M = keys, N = 16
+// queries) and O^T += V^T P^T (M = head dim, N = queries): with the
+// transposed products every lane owns one query, so the online-softmax
+// statistics and the O^T accumulator need no lane shuffles except the
+// 4-lane-group row max/sum.  Key rows inside the S^T tiles are permuted so
+// that a lane's P^T operand covers 8 consecutive keys, which are 8 consecutive
+// bf16 of one V^T row in the pool (kv_layout.h).
+//
+// Long rows may be split over several work items (split-KV); their partial
+// (O, max, sum) go to a workspace and a merge kernel combines them.  The host
+// planner orders work items longest first.
+#include <algorithm>
+#include <cmath>
+#include <numeric>
+#include <vector>
+
+#include "common.h"
+#include "kv_layout.h"
+
+namespace yapd {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kChunk = 32;  // keys per inner step (two pages)
+
+struct AttnParams {
+  const uint16_t* q;     // [rows, bl, H, 64]
+  const uint16_t* pool;  // [n_pages, 2, H, 1024]
+  int64_t n_pages;
+  const int32_t* table;
+  int table_stride, table_cols;
+  const int32_t* kv_len;
+  int rows, bl, H;
+  const int32_t* work;  // [n_work][4]: row, key_begin, key_end, slot (-1: final output)
+  float* part_o;        // [slots, bl, H, 64]
+  float* part_ml;       // [slots, bl, H, 2]
+  float scale_log2;     // softmax scale * log2(e)
+  uint16_t* out;        // [rows, bl, H, 64]
+};
+
+__device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <int NQT>
+__global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParams P) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * kWaves + wave;
+  const int4 it = reinterpret_cast<const int4*>(P.work)[blockIdx.x];
+  const int r = it.x, kb = it.y, ke = it.z, slot = it.w;
+  const int kvl = P.kv_len[r];
+  const int g = lane >> 4;   // lane group: key group / head-dim group
+  const int n = lane & 15;   // query within a 16-query tile / row within an M tile
+  const int H = P.H, bl = P.bl;
+
+  // Q^T fragments (B operand): lane holds Q[q = qt*16 + n][hd = ks*32 + 8g .. +7].
+  bf16x8_t qf[NQT][2];
+#pragma unroll
+  for (int qt = 0; qt < NQT; ++qt) {
+    const int q = qt * 16 + n;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (q < bl) v = load16(P.q + ((static_cast<int64_t>(r) * bl + q) * H + h) * kHeadDim + ks * 32 + 8 * g);
+      qf[qt][ks] = as_bf16x8(v);
+    }
+  }
+
+  f32x4_t o[NQT][4];
+  float m[NQT], l[NQT];
+#pragma unroll
+  for (int qt = 0; qt < NQT; ++qt) {
+    m[qt] = -INFINITY;
+    l[qt] = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[qt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int32_t* tab = P.table + static_cast<int64_t>(r) * P.table_stride;
+  // Page-table reads stay inside the row even if kv_len exceeds what the table maps.
+  const int last_page = min((kvl + kPageSize - 1) / kPageSize, P.table_cols) - 1;
+  // Key served by row n of S^T tile t: 8*(n/4) + 4t + n%4, so that lane group g
+  // ends up holding keys 8g .. 8g+7 of the chunk.
+  const int key_t0 = 8 * (n >> 2) + (n & 3);
+
+  for (int k0 = kb; k0 < ke; k0 += kChunk) {
+    const int pi0 = min(k0 / kPageSize, last_page);
+    int64_t p0 = tab[pi0];
+    int64_t p1 = tab[min(pi0 + 1, last_page)];
+    p0 = min(max(p0, int64_t{0}), P.n_pages - 1);  // a bad table entry cannot fault
+    p1 = min(max(p1, int64_t{0}), P.n_pages - 1);
+
+    // K fragments (A operand of S^T): tile t row n -> key key_t0 + 4t.
+    u32x4_t kf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key = key_t0 + 4 * t;
+      const int64_t pg = key < kPageSize ? p0 : p1;
+      const uint16_t* kp = P.pool + k_offset(pg, h, H, key & (kPageSize - 1), 8 * g);
+      kf[t][0] = load16(kp);
+      kf[t][1] = load16(kp + 32);
+    }
+    // V^T fragments (A operand of O^T): row hd = 16mt + n, keys 8g .. 8g+7.
+    u32x4_t vf[4];
+    {
+      const int64_t pg = g < 2 ? p0 : p1;
+      const uint16_t* vp = P.pool + v_offset(pg, h, H, 8 * (g & 1), n);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) vf[mt] = load16(vp + 16 * mt * kPageSize);
+    }
+    const bool tail = k0 + kChunk > kvl;
+    if (tail) {
+      // Keys past kv_len contribute P = 0; clear their V too so stale or
+      // uninitialised pool memory can never turn 0 * V into NaN.
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int key = k0 + 8 * g + 2 * w;
+          uint32_t x = vf[mt][w];
+          if (key >= kvl) x &= 0xffff0000u;
+          if (key + 1 >= kvl) x &= 0x0000ffffu;
+          vf[mt][w] = x;
+        }
+      }
+    }
+
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      f32x4_t s[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[t][0]), qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f},
+                                                       0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[t][1]), qf[qt][1], s[t], 0, 0, 0);
+      }
+      // s[t][j] = S[q = n][key 8g + 4t + j]
+      float sv[8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float x = s[t][j] * P.scale_log2;
+          if (tail && k0 + 8 * g + 4 * t + j >= kvl) x = -INFINITY;
+          sv[4 * t + j] = x;
+        }
+      }
+      float cm = sv[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) cm = fmaxf(cm, sv[i]);
+      cm = fmaxf(cm, shfl_xor_f(cm, 16));
+      cm = fmaxf(cm, shfl_xor_f(cm, 32));
+      const float mn = fmaxf(m[qt], cm);
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+      float ps = 0.f;
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(sv[i] - mn);
+        ps += p[i];
+      }
+      l[qt] = l[qt] * alpha + ps;
+      m[qt] = mn;
+      u32x4_t pw;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) pw[w] = pack_bf16x2(p[2 * w], p[2 * w + 1]);
+      const bf16x8_t pf = as_bf16x8(pw);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        o[qt][mt] *= alpha;
+        o[qt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vf[mt]), pf, o[qt][mt], 0, 0, 0);
+      }
+    }
+  }
+
+  // o[qt][mt][j] = O^T[hd = 16mt + 4g + j][q = qt*16 + n]
+#pragma unroll
+  for (int qt = 0; qt < NQT; ++qt) {
+    float L = l[qt];
+    L += shfl_xor_f(L, 16);
+    L += shfl_xor_f(L, 32);
+    const int q = qt * 16 + n;
+    if (q >= bl) continue;
+    const int64_t row_q = (static_cast<int64_t>(r) * bl + q) * H + h;
+    if (slot < 0) {
+      const float inv = 1.f / L;
+      uint16_t* op = P.out + row_q * kHeadDim + 4 * g;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        u32x2_t w2;
+        w2[0] = pack_bf16x2(o[qt][mt][0] * inv, o[qt][mt][1] * inv);
+        w2[1] = pack_bf16x2(o[qt][mt][2] * inv, o[qt][mt][3] * inv);
+        *reinterpret_cast<u32x2_t*>(op + 16 * mt) = w2;
+      }
+    } else {
+      const int64_t prow = (static_cast<int64_t>(slot) * bl + q) * H + h;
+      float* pp = P.part_o + prow * kHeadDim + 4 * g;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f32x4_t*>(pp + 16 * mt) = o[qt][mt];
+      if (g == 0) {
+        P.part_ml[prow * 2] = m[qt];
+        P.part_ml[prow * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+struct MergeParams {
+  const int32_t* merge;  // [n_merge][3]: row, first slot, n slots
+  const float* part_o;
+  const float* part_ml;
+  int bl, H;
+  uint16_t* out;
+};
+
+// One workgroup per (split row, query); a thread owns 4 head-dim values of one head.
+__global__ __launch_bounds__(256) void attn_merge_kernel(const MergeParams P) {
+  const int3 mi = make_int3(P.merge[blockIdx.x * 3], P.merge[blockIdx.x * 3 + 1], P.merge[blockIdx.x * 3 + 2]);
+  const int q = blockIdx.y;
+  for (int t = threadIdx.x; t < P.H * 16; t += blockDim.x) {
+    const int h = t >> 4;
+    const int d0 = (t & 15) * 4;
+    float M = -INFINITY;
+    for (int s = 0; s < mi.z; ++s) {
+      const int64_t prow = (static_cast<int64_t>(mi.y + s) * P.bl + q) * P.H + h;
+      M = fmaxf(M, P.part_ml[prow * 2]);
+    }
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+    for (int s = 0; s < mi.z; ++s) {
+      const int64_t prow = (static_cast<int64_t>(mi.y + s) * P.bl + q) * P.H + h;
+      const float w = __builtin_amdgcn_exp2f(P.part_ml[prow * 2] - M);
+      L += w * P.part_ml[prow * 2 + 1];
+      acc += w * *reinterpret_cast<const f32x4_t*>(P.part_o + prow * kHeadDim + d0);
+    }
+    const float inv = 1.f / L;
+    u32x2_t w2;
+    w2[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    w2[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    *reinterpret_cast<u32x2_t*>(P.out + ((static_cast<int64_t>(mi.x) * P.bl + q) * P.H + h) * kHeadDim + d0) = w2;
+  }
+}
+
+struct KvWriteParams {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t k_tok_stride, v_tok_stride;  // elements between consecutive tokens
+  uint16_t* pool;
+  int64_t n_pages;
+  const int32_t* table;
+  int table_stride, table_cols;
+  const int32_t* pos0;  // [rows] first position of the block
+  int rows, bl, H;
+};
+
+// Thread per (token, head, 8 head-dim values).
+__global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteParams P) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(P.rows) * P.bl * P.H * 8;
+  if (idx >= total) return;
+  const int d0 = static_cast<int>(idx & 7) * 8;
+  const int h = static_cast<int>((idx >> 3) % P.H);
+  const int64_t tok = (idx >> 3) / P.H;
+  const int r = static_cast<int>(tok / P.bl);
+  const int pos = P.pos0[r] + static_cast<int>(tok - static_cast<int64_t>(r) * P.bl);
+  const int pi = min(max(pos, 0) / kPageSize, P.table_cols - 1);
+  int64_t page = P.table[static_cast<int64_t>(r) * P.table_stride + pi];
+  page = min(max(page, int64_t{0}), P.n_pages - 1);
+  const int s = pos & (kPageSize - 1);
+  const u32x4_t kx = load16(P.k + tok * P.k_tok_stride + h * kHeadDim + d0);
+  *reinterpret_cast<u32x4_t*>(P.pool + k_offset(page, h, P.H, s, d0)) = kx;
+  const u32x4_t vx = load16(P.v + tok * P.v_tok_stride + h * kHeadDim + d0);
+  uint16_t* vp = P.pool + v_offset(page, h, P.H, s, d0);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    vp[(2 * w) * kPageSize] = static_cast<uint16_t>(vx[w] & 0xffffu);
+    vp[(2 * w + 1) * kPageSize] = static_cast<uint16_t>(vx[w] >> 16);
+  }
+}
+
+struct KvGatherParams {
+  const uint16_t* pool;
+  int64_t n_pages;
+  const int32_t* table_row;
+  int table_len, kv_len, H;
+  uint16_t* k_out;  // [kv_len, H, 64]
+  uint16_t* v_out;
+};
+
+__global__ __launch_bounds__(256) void kv_gather_kernel(const KvGatherParams P) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(P.kv_len) * P.H * kHeadDim;
+  if (idx >= total) return;
+  const int d = static_cast<int>(idx % kHeadDim);
+  const int h = static_cast<int>((idx / kHeadDim) % P.H);
+  const int pos = static_cast<int>(idx / (kHeadDim * P.H));
+  int64_t page = P.table_row[min(pos / kPageSize, P.table_len - 1)];
+  page = min(max(page, int64_t{0}), P.n_pages - 1);
+  const int s = pos & (kPageSize - 1);
+  P.k_out[idx] = P.pool[k_offset(page, h, P.H, s, d)];
+  P.v_out[idx] = P.pool[v_offset(page, h, P.H, s, d)];
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace yapd
+
+extern "C" int yapd_attn_plan(const int32_t* kv_len, int rows, int target_items, int min_split_keys,
+                              int32_t* work, int work_cap, int32_t* merge, int merge_cap, int* n_work, int* n_merge,
+                              int* n_slots) {
+  YAPD_REQUIRE(kv_len && work && merge && n_work && n_merge && n_slots, "attn_plan: NULL pointer");
+  YAPD_REQUIRE(rows >= 1 && target_items >= 1 && min_split_keys >= yapd::kChunk,
+               "attn_plan: need rows >= 1, target_items >= 1, min_split_keys >= 32");
+  const int unit = yapd::kChunk;
+  int64_t total_units = 0;
+  for (int r = 0; r < rows; ++r) {
+    YAPD_REQUIRE(kv_len[r] >= 1, "attn_plan: kv_len[%d] = %d < 1", r, kv_len[r]);
+    total_units += (kv_len[r] + unit - 1) / unit;
+  }
+  const int64_t min_units = min_split_keys / unit;
+  const int64_t per_item = std::max<int64_t>(min_units, (total_units + target_items - 1) / target_items);
+  struct Item {
+    int row, kb, ke, slot;
+  };
+  std::vector<Item> items;
+  std::vector<int32_t> mrg;
+  int slots = 0;
+  for (int r = 0; r < rows; ++r) {
+    const int units = (kv_len[r] + unit - 1) / unit;
+    const int splits = static_cast<int>(std::min<int64_t>(units, (units + per_item - 1) / per_item));
+    if (splits <= 1) {
+      items.push_back({r, 0, kv_len[r], -1});
+      continue;
+    }
+    const int base = units / splits, extra = units % splits;
+    int u = 0;
+    for (int s = 0; s < splits; ++s) {
+      const int take = base + (s < extra ? 1 : 0);
+      items.push_back({r, u * unit, std::min(kv_len[r], (u + take) * unit), slots + s});
+      u += take;
+    }
+    mrg.insert(mrg.end(), {r, slots, splits});
+    slots += splits;
+  }
+  // Longest first, so short items fill the tail of the launch.
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item& a, const Item& b) { return (a.ke - a.kb) > (b.ke - b.kb); });
+  YAPD_REQUIRE(static_cast<int>(items.size()) <= work_cap, "attn_plan: work_cap %d < %zu", work_cap, items.size());
+  YAPD_REQUIRE(static_cast<int>(mrg.size() / 3) <= merge_cap, "attn_plan: merge_cap %d < %zu", merge_cap,
+               mrg.size() / 3);
+  for (size_t i = 0; i < items.size(); ++i) {
+    work[4 * i] = items[i].row;
+    work[4 * i + 1] = items[i].kb;
+    work[4 * i + 2] = items[i].ke;
+    work[4 * i + 3] = items[i].slot;
+  }
+  std::copy(mrg.begin(), mrg.end(), merge);
+  *n_work = static_cast<int>(items.size());
+  *n_merge = static_cast<int>(mrg.size() / 3);
+  *n_slots = slots;
+  return YAPD_OK;
+}
+
+extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                                     int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads,
+                                     const int32_t* work, int n_work, const int32_t* merge, int n_merge,
+                                     float* part_o, float* part_ml, int n_slots, float scale, void* out,
+                                     void* stream) {
+  YAPD_REQUIRE(q && kv_pool && page_table && kv_len && work && out, "attn: NULL pointer");
+  YAPD_REQUIRE(yapd::aligned16(q) && yapd::aligned16(kv_pool) && yapd::aligned16(out) && yapd::aligned16(work),
+               "attn: q, kv_pool, out and work must be 16-byte aligned");
+  YAPD_REQUIRE(rows >= 1 && bl >= 1 && bl <= 64, "attn: need rows >= 1 and 1 <= bl <= 64 (got %d, %d)", rows, bl);
+  YAPD_REQUIRE(n_heads >= yapd::kWaves && n_heads % yapd::kWaves == 0, "attn: n_heads must be a multiple of %d",
+               yapd::kWaves);
+  YAPD_REQUIRE(n_pages >= 1 && table_cols >= 1 && table_stride >= table_cols, "attn: empty pool or table");
+  YAPD_REQUIRE(n_work >= 1 && n_work < (1 << 30), "attn: n_work = %d", n_work);
+  YAPD_REQUIRE(n_merge == 0 || (merge && part_o && part_ml && n_slots >= 1), "attn: split items need a workspace");
+  YAPD_REQUIRE(n_merge == 0 || (yapd::aligned16(part_o)), "attn: part_o must be 16-byte aligned");
+  yapd::AttnParams P;
+  P.q = static_cast<const uint16_t*>(q);
+  P.pool = static_cast<const uint16_t*>(kv_pool);
+  P.n_pages = n_pages;
+  P.table = page_table;
+  P.table_stride = table_stride;
+  P.table_cols = table_cols;
+  P.kv_len = kv_len;
+  P.rows = rows;
+  P.bl = bl;
+  P.H = n_heads;
+  P.work = work;
+  P.part_o = part_o;
+  P.part_ml = part_ml;
+  P.scale_log2 = scale * 1.4426950408889634f;
+  P.out = static_cast<uint16_t*>(out);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(n_work, n_heads / yapd::kWaves), block(64 * yapd::kWaves);
+  switch ((bl + 15) / 16) {
+    case 1: hipLaunchKernelGGL(yapd::attn_paged_kernel<1>, grid, block, 0, st, P); break;
+    case 2: hipLaunchKernelGGL(yapd::attn_paged_kernel<2>, grid, block, 0, st, P); break;
+    case 3: hipLaunchKernelGGL(yapd::attn_paged_kernel<3>, grid, block, 0, st, P); break;
+    default: hipLaunchKernelGGL(yapd::attn_paged_kernel<4>, grid, block, 0, st, P); break;
+  }
+  YAPD_LAUNCH_CHECK("attn_paged_kernel launch");
+  if (n_merge > 0) {
+    yapd::MergeParams M{merge, part_o, part_ml, bl, n_heads, static_cast<uint16_t*>(out)};
+    hipLaunchKernelGGL(yapd::attn_merge_kernel, dim3(n_merge, bl), dim3(256), 0, st, M);
+    YAPD_LAUNCH_CHECK("attn_merge_kernel launch");
+  }
+  return YAPD_OK;
+}
+
+extern "C" int yapd_kv_write(const void* k, const void* v, int64_t k_tok_stride, int64_t v_tok_stride, void* kv_pool,
+                             int64_t n_pages, const int32_t* page_table, int table_stride, int table_cols,
+                             const int32_t* pos0, int rows, int bl, int n_heads, void* stream) {
+  YAPD_REQUIRE(k && v && kv_pool && page_table && pos0, "kv_write: NULL pointer");
+  YAPD_REQUIRE(yapd::aligned16(k) && yapd::aligned16(v) && yapd::aligned16(kv_pool),
+               "kv_write: k, v, kv_pool must be 16-byte aligned");
+  YAPD_REQUIRE(k_tok_stride % 8 == 0 && v_tok_stride % 8 == 0, "kv_write: token strides must be multiples of 8");
+  YAPD_REQUIRE(rows >= 1 && bl >= 1 && n_heads >= 1 && n_pages >= 1, "kv_write: empty shape");
+  YAPD_REQUIRE(table_cols >= 1 && table_stride >= table_cols, "kv_write: bad table shape");
+  const int64_t total = static_cast<int64_t>(rows) * bl * n_heads * 8;
+  yapd::KvWriteParams P{static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), k_tok_stride, v_tok_stride,
+                        static_cast<uint16_t*>(kv_pool), n_pages, page_table, table_stride, table_cols, pos0, rows, bl,
+                        n_heads};
+  hipLaunchKernelGGL(yapd::kv_write_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), P);
+  YAPD_LAUNCH_CHECK("kv_write_kernel launch");
+  return YAPD_OK;
+}
+
+extern "C" int yapd_kv_gather(const void* kv_pool, int64_t n_pages, const int32_t* table_row, int table_len,
+                              int kv_len, int n_heads, void* k_out, void* v_out, void* stream) {
+  YAPD_REQUIRE(kv_pool && table_row && k_out && v_out, "kv_gather: NULL pointer");
+  YAPD_REQUIRE(kv_len >= 1 && n_heads >= 1 && n_pages >= 1 && table_len >= 1, "kv_gather: empty shape");
+  const int64_t total = static_cast<int64_t>(kv_len) * n_heads * yapd::kHeadDim;
+  yapd::KvGatherParams P{static_cast<const uint16_t*>(kv_pool), n_pages, table_row, table_len, kv_len, n_heads,
+                         static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out)};
+  hipLaunchKernelGGL(yapd::kv_gather_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), P);
+  YAPD_LAUNCH_CHECK("kv_gather_kernel launch");
+  return YAPD_OK;
+}

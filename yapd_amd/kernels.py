@@ -32,6 +32,13 @@ _SIGNATURES = {
         c_void, c_i64, c_i64, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
         c_void, c_void, c_void, c_void, c_void, c_void, c_int, c_float, c_int, c_i64, c_i64,
         c_float, c_int, c_u64, c_u64, c_void, c_void, c_void, c_void, c_void, c_void, c_void]),
+    "yapd_attn_plan": (c_int, [c_void, c_int, c_int, c_int, c_void, c_int, c_void, c_int, c_void, c_void, c_void]),
+    "yapd_attn_paged_block": (c_int, [
+        c_void, c_void, c_i64, c_void, c_int, c_int, c_void, c_int, c_int, c_int, c_void, c_int, c_void, c_int,
+        c_void, c_void, c_int, c_float, c_void, c_void]),
+    "yapd_kv_write": (c_int, [c_void, c_void, c_i64, c_i64, c_void, c_i64, c_void, c_int, c_int, c_void, c_int,
+                              c_int, c_int, c_void]),
+    "yapd_kv_gather": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_void]),
 }
 
 
@@ -140,3 +147,97 @@ def score_cfg_pmi_unmask(
         out["sampled"].data_ptr(), out["pmi"].data_ptr(), out["unmask"].data_ptr(),
         out["xt_out"].data_ptr(), out["n_mask_after"].data_ptr(), out["hit_eos"].data_ptr(),
         stream_ptr(dev)))
+
+
+# --------------------------------------------------------------------------- #
+# (a) paged block attention
+# --------------------------------------------------------------------------- #
+
+def attn_plan(kv_len, target_items: int = 1024, min_split_keys: int = 128):
+    """Host planner: ``(work [n,4] int32, merge [m,3] int32, n_slots)`` numpy arrays.
+
+    Rows are cut into work items of whole 32-key chunks so that about
+    ``target_items`` items exist; items are ordered longest first.
+    """
+    import numpy as np
+    kv = np.ascontiguousarray(np.asarray(kv_len, dtype=np.int32))
+    rows = int(kv.size)
+    unit = 32
+    cap = int(sum((int(x) + unit - 1) // unit for x in kv)) + rows
+    work = np.zeros((cap, 4), dtype=np.int32)
+    merge = np.zeros((rows, 3), dtype=np.int32)
+    nw, nm, ns = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(load_library().yapd_attn_plan(
+        kv.ctypes.data, rows, int(target_items), int(min_split_keys), work.ctypes.data, cap,
+        merge.ctypes.data, rows, ctypes.byref(nw), ctypes.byref(nm), ctypes.byref(ns)))
+    return work[: nw.value].copy(), merge[: nm.value].copy(), ns.value
+
+
+def attn_paged_block(q: torch.Tensor, pool: torch.Tensor, table: torch.Tensor, kv_len: torch.Tensor,
+                     work: torch.Tensor, merge: Optional[torch.Tensor], part_o: Optional[torch.Tensor],
+                     part_ml: Optional[torch.Tensor], out: torch.Tensor, scale: float) -> None:
+    """``out [rows, bl, H, 64] = softmax(q K^T * scale) V`` over each row's pages."""
+    dev = q.device
+    require_cuda(q, "q", torch.bfloat16, dev)
+    require(q.dim() == 4 and q.shape[3] == 64, "q must be [rows, bl, H, 64]")
+    rows, bl, H, _ = q.shape
+    require_cuda(pool, "pool", torch.bfloat16, dev)
+    require(pool.dim() == 4 and pool.shape[1] == 2 and pool.shape[2] == H and pool.shape[3] == 1024,
+            "pool must be [pages, 2, H, 16*64]")
+    require_cuda(table, "table", torch.int32, dev, contiguous=False)
+    require(table.dim() == 2 and table.shape[0] >= rows and table.stride(1) == 1,
+            "table must be [>= rows, max_pages] with unit column stride")
+    require_cuda(kv_len, "kv_len", torch.int32, dev)
+    require(kv_len.numel() >= rows, "kv_len must have rows entries")
+    require_cuda(work, "work", torch.int32, dev)
+    require(work.dim() == 2 and work.shape[1] == 4, "work must be [n, 4]")
+    n_merge = 0 if merge is None else int(merge.shape[0])
+    n_slots = 0
+    if n_merge:
+        require_cuda(merge, "merge", torch.int32, dev)
+        require_cuda(part_o, "part_o", torch.float32, dev)
+        require_cuda(part_ml, "part_ml", torch.float32, dev)
+        n_slots = int(part_o.shape[0])
+        require(tuple(part_o.shape[1:]) == (bl, H, 64) and tuple(part_ml.shape) == (n_slots, bl, H, 2),
+                "part_o/part_ml shapes")
+    require_cuda(out, "out", torch.bfloat16, dev)
+    require(tuple(out.shape) == (rows, bl, H, 64), "out must match q")
+    check(load_library().yapd_attn_paged_block(
+        q.data_ptr(), pool.data_ptr(), pool.shape[0], table.data_ptr(), table.stride(0), table.shape[1],
+        kv_len.data_ptr(),
+        rows, bl, H, work.data_ptr(), int(work.shape[0]), ptr(merge), n_merge, ptr(part_o), ptr(part_ml),
+        n_slots, float(scale), out.data_ptr(), stream_ptr(dev)))
+
+
+def kv_write(k: torch.Tensor, v: torch.Tensor, pool: torch.Tensor, table: torch.Tensor,
+             pos0: torch.Tensor, bl: int) -> None:
+    """Scatter ``k, v`` (``[rows*bl, H, 64]`` views, unit last strides) into the pages."""
+    dev = k.device
+    for name, t in (("k", k), ("v", v)):
+        require_cuda(t, name, torch.bfloat16, dev, contiguous=False)
+        require(t.dim() == 3 and t.shape[2] == 64 and t.stride(2) == 1 and t.stride(1) == 64,
+                f"{name} must be [tokens, H, 64] with packed heads")
+    H = k.shape[1]
+    require_cuda(pool, "pool", torch.bfloat16, dev)
+    require(pool.dim() == 4 and pool.shape[2] == H and pool.shape[3] == 1024, "pool must be [pages, 2, H, 1024]")
+    require_cuda(table, "table", torch.int32, dev)
+    require_cuda(pos0, "pos0", torch.int32, dev)
+    rows = int(pos0.numel())
+    require(k.shape[0] == rows * bl and v.shape[0] == rows * bl, "k/v must hold rows*bl tokens")
+    check(load_library().yapd_kv_write(
+        k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), pool.data_ptr(), pool.shape[0],
+        table.data_ptr(), table.stride(0), table.shape[1], pos0.data_ptr(), rows, bl, H, stream_ptr(dev)))
+
+
+def kv_gather(pool: torch.Tensor, table_row: torch.Tensor, kv_len: int):
+    """Dense ``K, V [kv_len, H, 64]`` of one row (page-table gather, debug/test path)."""
+    dev = pool.device
+    require_cuda(pool, "pool", torch.bfloat16, dev)
+    require_cuda(table_row, "table_row", torch.int32, dev)
+    H = pool.shape[2]
+    require(table_row.numel() * 16 >= kv_len, "table_row too short for kv_len")
+    k = torch.empty(kv_len, H, 64, dtype=torch.bfloat16, device=dev)
+    v = torch.empty_like(k)
+    check(load_library().yapd_kv_gather(pool.data_ptr(), pool.shape[0], table_row.data_ptr(), table_row.numel(),
+                                        int(kv_len), H, k.data_ptr(), v.data_ptr(), stream_ptr(dev)))
+    return k, v
