@@ -72,6 +72,143 @@ int yapd_score_cfg_pmi_unmask(
     int64_t* sampled_out, float* pmi_out, uint8_t* unmask_out, int64_t* xt_out,
     int32_t* n_mask_after_out, uint8_t* hit_eos_out, void* stream);
 
+
+/* ------------------------------------------------------------------------ *
+ * Paged KV pool (one per layer): bf16 [n_pages][2][H][16*64]; plane 0 holds
+ * K (token-major inside a head), plane 1 holds V transposed inside a head.
+ * Position p of row r lives on page page_table[r*table_stride + p/16], slot
+ * p % 16.  Replaces the NHD pool + static page slices of
+ * engines/flashinfer.py:104-116 and the index math of :318-344; any
+ * permutation of pool pages is a valid table.  Table reads are clamped to
+ * table_cols entries and page ids to n_pages, so a bad table cannot fault.
+ * ------------------------------------------------------------------------ */
+
+/* Scatter k, v ([rows*bl, H, 64] with token strides k_tok_stride,
+ * v_tok_stride) at positions pos0[r] .. pos0[r]+bl-1 (device int32).
+ * Replaces paged_kv[li][pw_idx, 0|1, pw_off] = k|v (engines/flashinfer.py:1034-1035). */
+int yapd_kv_write(const void* k, const void* v, int64_t k_tok_stride, int64_t v_tok_stride, void* kv_pool,
+                  int64_t n_pages, const int32_t* page_table, int table_stride, int table_cols,
+                  const int32_t* pos0, int rows, int bl, int n_heads, void* stream);
+
+/* Debug/test gather of one row's K and V, dense [kv_len, H, 64] each. */
+int yapd_kv_gather(const void* kv_pool, int64_t n_pages, const int32_t* table_row, int table_len, int kv_len,
+                   int n_heads, void* k_out, void* v_out, void* stream);
+
+/* Host-side planner (CPU only, no GPU call): cuts each row's kv_len keys
+ * into work items of whole 32-key chunks so that ~target_items items exist,
+ * longest first.  work [n_work][4] = (row, key_begin, key_end, slot; slot -1
+ * means the item writes the final output), merge [n_merge][3] = (row,
+ * first_slot, n_slots).  Replaces the per-block plan() of
+ * engines/flashinfer.py:346-411. */
+int yapd_attn_plan(const int32_t* kv_len, int rows, int target_items, int min_split_keys, int32_t* work,
+                   int work_cap, int32_t* merge, int merge_cap, int* n_work, int* n_merge, int* n_slots);
+
+/* (a) Block attention over paged KV: out[r, i] = softmax(q[r, i] K_r^T *
+ * scale) V_r over keys [0, kv_len[r]) -- bidirectional over the whole block
+ * (causal = 0, the block step: engines/flashinfer.py:884-886, 1037-1039;
+ * torch_sdpa.py:299-307), or causal inside the block (causal = 1, prefix
+ * prefill).  q, out: bf16 [rows, bl, H, 64]; kv_len on the device.
+ * n_work / n_merge size the grids; counts (device {n_work, n_merge}, may be
+ * NULL) lets a captured graph replay with fewer items.  part_o [n_slots, bl,
+ * H, 64] and part_ml [n_slots, bl, H, 2] fp32 are the split-KV workspace. */
+int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                          int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads,
+                          const int32_t* work, int n_work, const int32_t* merge, int n_merge,
+                          const int32_t* counts, float* part_o, float* part_ml, int n_slots, float scale,
+                          int causal, void* out, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * (b) bf16 MFMA projections (nn.Linear layout: C = A W^T, fp32 accumulate).
+ * K must be a multiple of 64; A, W 16-byte aligned with leading dims
+ * multiples of 8.
+ * ------------------------------------------------------------------------ */
+
+/* Plain projection: o_proj / down_proj (F.linear at engines/flashinfer.py:1041, 455). */
+int yapd_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, int M, int N, int K, void* C,
+                   int64_t ldc, void* stream);
+
+/* Fused QKV + NeoX RoPE + paged KV write (engines/flashinfer.py:998-1035):
+ * rows r*bl+j at position pos0[r]+j; cos/sin fp32 [max_pos, 64] hold the
+ * model-dtype table (flashinfer.py:246-255); q goes to q_out [M, H*64], k
+ * and v straight into the pool. */
+int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
+                          const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int bl,
+                          void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride,
+                          int table_cols, void* stream);
+
+/* Fused gate/up + SiLU*up (engines/flashinfer.py:433-455): W rows are
+ * [gate f..f+31; up f..f+31] for f = 0, 32, ...; act [M, F]. */
+int yapd_gemm_swiglu(const void* A, int64_t lda, const void* W_gu_interleaved, int M, int F, int K, void* act,
+                     int64_t ld_act, void* stream);
+
+/* Token-shifted speech head (engines/flashinfer.py:1452-1461): logits row
+ * (r, j) = W hidden[r, j-1], and (r, 0) = W shift_ctx[r]. */
+int yapd_gemm_head_shift(const void* hidden, const void* shift_ctx, int rows, int bl, int K, const void* W,
+                         int64_t ldw, int N, void* logits, int64_t ldc, void* stream);
+
+/* HF LlamaRMSNorm rows (D multiple of 512, <= 2048): out = w * bf16(x *
+ * rsqrt(mean(x^2) + eps)).  With delta: residual = bf16(residual + delta)
+ * in place first (flashinfer fused_add_rmsnorm, engines/flashinfer.py:1043-1060);
+ * with x and residual: residual = x (the clone of engines/flashinfer.py:992). */
+int yapd_rmsnorm(const void* delta, void* residual, const void* x, const void* w, float eps, int M, int D,
+                 void* out, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Whole block forward: one call runs the n_layers decoder layers and the
+ * final norm (engines/flashinfer.py:_block_forward_fused :970-1065 /
+ * _graph_body :1312-1461), optionally followed by the token-shifted head.
+ * ------------------------------------------------------------------------ */
+typedef struct yapd_t3_layer {
+  const void* w_qkv;     /* bf16 [3*H*64, D]: q, k, v rows */
+  const void* w_o;       /* bf16 [D, H*64] */
+  const void* w_gate_up; /* bf16 [2F, D], gate/up interleaved per 32 rows */
+  const void* w_down;    /* bf16 [D, F] */
+  const void* ln_in;     /* bf16 [D] */
+  const void* ln_post;   /* bf16 [D] */
+  float eps_in, eps_post;
+  void* kv_pool;         /* this layer's pool */
+} yapd_t3_layer;
+
+typedef struct yapd_t3_model {
+  int n_layers, hidden, n_heads, ffn;
+  const yapd_t3_layer* layers; /* host array [n_layers] */
+  const void* final_norm;      /* bf16 [D] */
+  float final_eps;
+  const float* rope_cos;       /* fp32 [rope_positions, 64] */
+  const float* rope_sin;
+  int rope_positions;
+  int64_t n_pages;
+  const int32_t* page_table;
+  int table_stride, table_cols;
+} yapd_t3_model;
+
+typedef struct yapd_t3_workspace {
+  void* residual; /* bf16 [rows*bl, D] */
+  void* q;        /* bf16 [rows*bl, H*64] */
+  void* attn;     /* bf16 [rows*bl, H*64] */
+  void* normed;   /* bf16 [rows*bl, D] */
+  void* delta;    /* bf16 [rows*bl, D] */
+  void* act;      /* bf16 [rows*bl, F] */
+  const int32_t* work;   /* attention plan (yapd_attn_plan), device */
+  int n_work;
+  const int32_t* merge;
+  int n_merge;
+  const int32_t* counts; /* device {n_work, n_merge} or NULL */
+  float* part_o;
+  float* part_ml;
+  int n_slots;
+} yapd_t3_workspace;
+
+/* block_emb [rows*bl, D] is not modified; pos0 [rows] (device) is each row's
+ * first position, kv_len [rows] (device) = pos0 + bl.  hidden_out [rows*bl,
+ * D] receives the final-normed hidden.  If head_w != NULL the logits [rows,
+ * bl, vocab] (row pitch ld_logits) are computed from hidden and shift_ctx
+ * [rows, D]. */
+int yapd_t3_block_forward(const yapd_t3_model* model, const yapd_t3_workspace* ws, const void* block_emb,
+                          int rows, int bl, const int32_t* pos0, const int32_t* kv_len, int causal,
+                          void* hidden_out, const void* head_w, int vocab, const void* shift_ctx, void* logits,
+                          int64_t ld_logits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,130 @@
+"""GPU numerics of the bf16 MFMA GEMM family (b) and the RMSNorm rows against
+plain PyTorch fp32 references with the reference's bf16 rounding points
+(engines/flashinfer.py:433-455, 970-1065; HF LlamaRMSNorm, apply_rotary_pos_emb)."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import llama as OL
+from oracle import pages as OP
+from yapd_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def rnd(*shape, std=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).bfloat16()
+
+
+def rel_err(out, ref):
+    return ((out.float() - ref.float()).abs().max() / ref.float().abs().max().clamp_min(1e-6)).item()
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 3072, 1024), (1024, 1024, 4096), (37, 8194, 1024),
+                                   (16384 // 8, 8192, 1024)])
+def test_gemm_bf16(dev, M, N, K):
+    A = rnd(M, K, seed=1)
+    W = rnd(N, K, std=0.02, seed=2)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    kernels.gemm_bf16(A.to(dev), W.to(dev), out)
+    ref = A.float() @ W.float().T
+    assert rel_err(out.cpu(), ref) <= 8e-3
+
+
+def test_gemm_padded_ldc_and_strided_a(dev):
+    M, N, K = 96, 300, 256
+    base = rnd(M, K + 64, seed=3).to(dev)
+    A = base[:, 32: 32 + K]
+    W = rnd(N, K, std=0.05, seed=4).to(dev)
+    out_full = torch.zeros(M, 312, dtype=torch.bfloat16, device=dev)
+    out = out_full[:, :N]
+    kernels.gemm_bf16(A, W, out)
+    ref = A.float().cpu() @ W.float().cpu().T
+    assert rel_err(out.cpu(), ref) <= 8e-3
+    assert torch.count_nonzero(out_full[:, N:]) == 0  # nothing written past N
+
+
+def test_gemm_swiglu(dev):
+    M, K, Fd = 300, 1024, 4096
+    A = rnd(M, K, seed=5)
+    Wg = rnd(Fd, K, std=0.02, seed=6)
+    Wu = rnd(Fd, K, std=0.02, seed=7)
+    act = torch.empty(M, Fd, dtype=torch.bfloat16, device=dev)
+    kernels.gemm_swiglu(A.to(dev), kernels.interleave_gate_up(Wg, Wu).to(dev), act)
+    g = (A.float() @ Wg.float().T).bfloat16()
+    u = (A.float() @ Wu.float().T).bfloat16()
+    ref = (F.silu(g.float()).bfloat16().float() * u.float()).bfloat16()
+    assert rel_err(act.cpu(), ref.float()) <= 1.5e-2
+
+
+def test_gemm_head_shift(dev):
+    rows, bl, D, V = 6, 32, 1024, 8194
+    hidden = rnd(rows, bl, D, seed=8)
+    ctx = rnd(rows, 1, D, seed=9)
+    W = rnd(V, D, std=0.02, seed=10)
+    logits = torch.empty(rows, bl, 8200, dtype=torch.bfloat16, device=dev)[..., :V]
+    kernels.gemm_head_shift(hidden.to(dev), ctx.to(dev), W.to(dev), logits)
+    ref = OL.speech_head_shift(hidden.float(), ctx.float(), W.float())
+    assert rel_err(logits.cpu(), ref) <= 8e-3
+
+
+def test_gemm_qkv_rope_kv(dev):
+    from types import SimpleNamespace
+    from tests.test_oracle_llama import tiny_model  # noqa: F401 (rotary table helper below)
+    H, D, rows, bl = 16, 1024, 3, 32
+    M = rows * bl
+    A = rnd(M, D, seed=11)
+    Wqkv = rnd(3 * H * 64, D, std=0.02, seed=12)
+    pos0 = [7, 150, 600]
+    # HF default RoPE table (theta 10000) in the model dtype, as the engine builds it
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
+    t = torch.arange(1024).float()
+    fr = torch.outer(t, inv)
+    emb = torch.cat([fr, fr], -1)
+    cos_b, sin_b = emb.cos().bfloat16(), emb.sin().bfloat16()
+    n_pages = 160
+    table = np.random.default_rng(0).permutation(n_pages)[: rows * 48].reshape(rows, 48).astype(np.int32)
+    pool = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
+    q_out = torch.empty(M, H * 64, dtype=torch.bfloat16, device=dev)
+    kernels.gemm_qkv_rope_kv(A.to(dev), Wqkv.to(dev), cos_b.float().to(dev), sin_b.float().to(dev),
+                             torch.tensor(pos0, dtype=torch.int32, device=dev), bl, q_out, pool,
+                             torch.from_numpy(table).to(dev))
+    qkv = (A.float() @ Wqkv.float().T).bfloat16()
+    q = qkv[:, : H * 64].view(rows, bl, H, 64)
+    k = qkv[:, H * 64: 2 * H * 64].view(rows, bl, H, 64)
+    v = qkv[:, 2 * H * 64:].view(M, H, 64)
+    pos = torch.stack([torch.arange(p, p + bl) for p in pos0])
+    q = OL.rope(q, cos_b[pos], sin_b[pos])
+    k = OL.rope(k, cos_b[pos], sin_b[pos]).reshape(M, H, 64)
+    assert rel_err(q_out.cpu().view(rows, bl, H, 64), q.float()) <= 1.6e-2
+    pool_ref = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16)
+    OP.pool_write(pool_ref, table, pos0, k, v)
+    assert rel_err(pool.cpu(), pool_ref.float()) <= 1.6e-2
+    # slots outside the block positions stay untouched
+    touched = pool_ref.abs().sum(-1) > 0
+    assert torch.count_nonzero(pool.cpu().float().abs().sum(-1)[~touched]) == 0
+
+
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_rmsnorm(dev, with_delta):
+    M, D = 333, 1024
+    x = rnd(M, D, seed=13) * 3
+    w = (torch.rand(D, generator=torch.Generator().manual_seed(14)) + 0.5).bfloat16()
+    delta = rnd(M, D, seed=15)
+    out = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    xd = x.to(dev)
+    if with_delta:
+        kernels.rmsnorm(xd, w.to(dev), 1e-5, out, delta=delta.to(dev))
+        res = x + delta  # bf16 add, as the decoder layer's residual
+        assert torch.equal(xd.cpu(), res)
+    else:
+        kernels.rmsnorm(xd, w.to(dev), 1e-5, out)
+        res = x
+    ref = OL.rms_norm(res, w, 1e-5)
+    diff = (out.cpu().float() - ref.float()).abs()
+    ulp = ref.float().abs() * 2 ** -7 + 1e-6
+    assert (diff <= ulp).all()
+    assert (diff > 0).float().mean().item() < 0.01  # all but a few match bit for bit

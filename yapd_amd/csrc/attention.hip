@@ -43,9 +43,11 @@ struct AttnParams {
   const int32_t* kv_len;
   int rows, bl, H;
   const int32_t* work;  // [n_work][4]: row, key_begin, key_end, slot (-1: final output)
+  const int32_t* counts;  // optional device {n_work, n_merge}: grids sized by upper bounds (graph replay)
   float* part_o;        // [slots, bl, H, 64]
   float* part_ml;       // [slots, bl, H, 2]
   float scale_log2;     // softmax scale * log2(e)
+  int causal;           // 1: query i of the block sees keys < kv_len - bl + i + 1 (prefix prefill)
   uint16_t* out;        // [rows, bl, H, 64]
 };
 
@@ -60,6 +62,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int h = blockIdx.y * kWaves + wave;
+  if (P.counts != nullptr && static_cast<int>(blockIdx.x) >= P.counts[0]) return;
   const int4 it = reinterpret_cast<const int4*>(P.work)[blockIdx.x];
   const int r = it.x, kb = it.y, ke = it.z, slot = it.w;
   const int kvl = P.kv_len[r];
@@ -123,6 +126,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
       for (int mt = 0; mt < 4; ++mt) vf[mt] = load16(vp + 16 * mt * kPageSize);
     }
     const bool tail = k0 + kChunk > kvl;
+    const int diag0 = kvl - bl;  // causal: query q may see keys <= diag0 + q
+    const bool mask_chunk = tail || (P.causal && k0 + kChunk > diag0 + 1);
     if (tail) {
       // Keys past kv_len contribute P = 0; clear their V too so stale or
       // uninitialised pool memory can never turn 0 * V into NaN.
@@ -155,7 +160,10 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float x = s[t][j] * P.scale_log2;
-          if (tail && k0 + 8 * g + 4 * t + j >= kvl) x = -INFINITY;
+          if (mask_chunk) {
+            const int key = k0 + 8 * g + 4 * t + j;
+            if (key >= kvl || (P.causal && key > diag0 + qt * 16 + n)) x = -INFINITY;
+          }
           sv[4 * t + j] = x;
         }
       }
@@ -221,6 +229,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
 
 struct MergeParams {
   const int32_t* merge;  // [n_merge][3]: row, first slot, n slots
+  const int32_t* counts;
   const float* part_o;
   const float* part_ml;
   int bl, H;
@@ -229,6 +238,7 @@ struct MergeParams {
 
 // One workgroup per (split row, query); a thread owns 4 head-dim values of one head.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const MergeParams P) {
+  if (P.counts != nullptr && static_cast<int>(blockIdx.x) >= P.counts[1]) return;
   const int3 mi = make_int3(P.merge[blockIdx.x * 3], P.merge[blockIdx.x * 3 + 1], P.merge[blockIdx.x * 3 + 2]);
   const int q = blockIdx.y;
   for (int t = threadIdx.x; t < P.H * 16; t += blockDim.x) {
@@ -379,8 +389,8 @@ extern "C" int yapd_attn_plan(const int32_t* kv_len, int rows, int target_items,
 extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
                                      int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads,
                                      const int32_t* work, int n_work, const int32_t* merge, int n_merge,
-                                     float* part_o, float* part_ml, int n_slots, float scale, void* out,
-                                     void* stream) {
+                                     const int32_t* counts, float* part_o, float* part_ml, int n_slots,
+                                     float scale, int causal, void* out, void* stream) {
   YAPD_REQUIRE(q && kv_pool && page_table && kv_len && work && out, "attn: NULL pointer");
   YAPD_REQUIRE(yapd::aligned16(q) && yapd::aligned16(kv_pool) && yapd::aligned16(out) && yapd::aligned16(work),
                "attn: q, kv_pool, out and work must be 16-byte aligned");
@@ -403,9 +413,11 @@ extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t
   P.bl = bl;
   P.H = n_heads;
   P.work = work;
+  P.counts = counts;
   P.part_o = part_o;
   P.part_ml = part_ml;
   P.scale_log2 = scale * 1.4426950408889634f;
+  P.causal = causal != 0;
   P.out = static_cast<uint16_t*>(out);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(n_work, n_heads / yapd::kWaves), block(64 * yapd::kWaves);
@@ -417,7 +429,7 @@ extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t
   }
   YAPD_LAUNCH_CHECK("attn_paged_kernel launch");
   if (n_merge > 0) {
-    yapd::MergeParams M{merge, part_o, part_ml, bl, n_heads, static_cast<uint16_t*>(out)};
+    yapd::MergeParams M{merge, counts, part_o, part_ml, bl, n_heads, static_cast<uint16_t*>(out)};
     hipLaunchKernelGGL(yapd::attn_merge_kernel, dim3(n_merge, bl), dim3(256), 0, st, M);
     YAPD_LAUNCH_CHECK("attn_merge_kernel launch");
   }

@@ -1,0 +1,57 @@
+// Whole-block forward of the T3 backbone: the layer loop of
+// engines/flashinfer.py:_block_forward_fused (:970-1065) / _graph_body
+// (:1312-1461) driven from native code, one FFI call per step.  Every launch
+// goes to the caller's stream, so the whole call can be captured in a HIP
+// graph.
+//
+// Per layer:  qkv+rope+kv-write GEMM -> paged attention -> o_proj GEMM ->
+//             residual add + post-attention RMSNorm -> gate/up+SiLU GEMM ->
+//             down GEMM -> residual add + next input RMSNorm (final norm
+//             after the last layer).
+#include "common.h"
+
+#define YAPD_TRY(expr)            \
+  do {                            \
+    const int _rc = (expr);       \
+    if (_rc != YAPD_OK) return _rc; \
+  } while (0)
+
+extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* block_emb,
+                                     int rows, int bl, const int32_t* pos0, const int32_t* kv_len, int causal,
+                                     void* hidden_out, const void* head_w, int vocab, const void* shift_ctx,
+                                     void* logits, int64_t ld_logits, void* stream) {
+  YAPD_REQUIRE(m && ws && block_emb && pos0 && kv_len && hidden_out, "t3_block_forward: NULL pointer");
+  YAPD_REQUIRE(m->n_layers >= 1 && m->layers, "t3_block_forward: no layers");
+  YAPD_REQUIRE(rows >= 1 && bl >= 1 && bl <= 64, "t3_block_forward: need rows >= 1, 1 <= bl <= 64");
+  YAPD_REQUIRE(ws->residual && ws->q && ws->attn && ws->normed && ws->delta && ws->act && ws->work,
+               "t3_block_forward: incomplete workspace");
+  const int D = m->hidden, H = m->n_heads, F = m->ffn, HD = H * 64;
+  const int M = rows * bl;
+  const float scale = 0.125f;  // head_dim ** -0.5 for head_dim 64
+  void* st = stream;
+  auto* res = ws->residual;
+  auto* xn = ws->normed;
+
+  YAPD_TRY(yapd_rmsnorm(nullptr, res, block_emb, m->layers[0].ln_in, m->layers[0].eps_in, M, D, xn, st));
+  for (int li = 0; li < m->n_layers; ++li) {
+    const yapd_t3_layer& L = m->layers[li];
+    YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0, bl,
+                                   ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, st));
+    YAPD_TRY(yapd_attn_paged_block(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols,
+                                   kv_len, rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts,
+                                   ws->part_o, ws->part_ml, ws->n_slots, scale, causal, ws->attn, st));
+    YAPD_TRY(yapd_gemm_bf16(ws->attn, HD, L.w_o, HD, M, D, HD, ws->delta, D, st));
+    YAPD_TRY(yapd_rmsnorm(ws->delta, res, nullptr, L.ln_post, L.eps_post, M, D, xn, st));
+    YAPD_TRY(yapd_gemm_swiglu(xn, D, L.w_gate_up, M, F, D, ws->act, F, st));
+    YAPD_TRY(yapd_gemm_bf16(ws->act, F, L.w_down, F, M, D, F, ws->delta, D, st));
+    const bool last = li + 1 == m->n_layers;
+    const void* wn = last ? m->final_norm : m->layers[li + 1].ln_in;
+    const float eps = last ? m->final_eps : m->layers[li + 1].eps_in;
+    YAPD_TRY(yapd_rmsnorm(ws->delta, res, nullptr, wn, eps, M, D, last ? hidden_out : xn, st));
+  }
+  if (head_w != nullptr) {
+    YAPD_REQUIRE(shift_ctx && logits && vocab >= 1, "t3_block_forward: head needs shift_ctx and logits");
+    YAPD_TRY(yapd_gemm_head_shift(hidden_out, shift_ctx, rows, bl, D, head_w, D, vocab, logits, ld_logits, st));
+  }
+  return YAPD_OK;
+}

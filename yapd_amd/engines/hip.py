@@ -1,0 +1,404 @@
+"""``HipEngine``: the MI355X (gfx950) block-diffusion engine.
+
+Implements the engine protocol of chatterbox_flash/engines/base.py:42-141 as
+a drop-in next to FlashInferEngine (engines/flashinfer.py:56-1563):
+
+* paged KV per layer (any page table; static per-row slices by default, as
+  engines/flashinfer.py:104-116), bf16, written by the fused QKV epilogue;
+* ``block_forward`` = one native call (``yapd_t3_block_forward``) running the
+  30 decoder layers and the final norm on the caller's stream;
+* ``capture_cuda_graph`` captures that call plus the token-shifted speech
+  head in a HIP graph (engines/flashinfer.py:1147-1310); ``block_forward_graph``
+  replays it and returns views of persistent buffers
+  (engines/flashinfer.py:1477-1563);
+* ``prefix_forward`` prefills the conditioning prefix with the same kernels,
+  causal inside 64-token chunks (engines/flashinfer.py:678-854 does it with
+  a ragged FlashInfer prefill).
+
+Only bf16 is supported (the deployed dtype); other dtypes raise ValueError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+import math
+from typing import Dict, List, Optional, Tuple, Union
+
+import torch
+from torch import Tensor
+
+from .. import kernels
+from ..paged import PAGE_SIZE, AttnPlan, PagedKV
+
+logger = logging.getLogger(__name__)
+
+CacheStarts = Union[int, List[int]]
+PREFILL_CHUNK = 64
+
+
+class _Buffers:
+    """Per-(rows, bl) activations; persistent so a captured graph can replay."""
+
+    def __init__(self, rows: int, bl: int, D: int, H: int, F: int, dev: torch.device):
+        N = rows * bl
+        bf = torch.bfloat16
+        self.rows, self.bl = rows, bl
+        self.emb = torch.zeros(N, D, dtype=bf, device=dev)
+        self.residual = torch.empty(N, D, dtype=bf, device=dev)
+        self.q = torch.empty(N, H * 64, dtype=bf, device=dev)
+        self.attn = torch.empty(N, H * 64, dtype=bf, device=dev)
+        self.normed = torch.empty(N, D, dtype=bf, device=dev)
+        self.delta = torch.empty(N, D, dtype=bf, device=dev)
+        self.act = torch.empty(N, F, dtype=bf, device=dev)
+        self.hidden = torch.empty(N, D, dtype=bf, device=dev)
+        self.pos0 = torch.zeros(rows, dtype=torch.int32, device=dev)
+
+
+class HipEngine:
+    """Paged-KV engine on hand-written gfx950 kernels (``backend="hip"``)."""
+
+    def __init__(self, model, max_seq_len: int, dtype: torch.dtype, *, batch_size: int = 1,
+                 page_size: int = 16, page_table_seed: Optional[int] = None, attn_target_items: int = 192):
+        if dtype != torch.bfloat16:
+            raise ValueError(f"HipEngine runs bf16 only; got {dtype}")
+        if page_size != PAGE_SIZE:
+            raise ValueError(f"HipEngine uses {PAGE_SIZE}-token pages; got page_size={page_size}")
+        kernels.load_library()
+        tf = model.tfmr
+        cfg = tf.config
+        dev = torch.device(getattr(model, "device", tf.norm.weight.device))
+        if dev.type != "cuda":
+            raise ValueError("HipEngine needs the model on a GPU")
+        H = cfg.num_attention_heads
+        Hkv = cfg.num_key_value_heads
+        hd = getattr(cfg, "head_dim", None) or cfg.hidden_size // H
+        D = cfg.hidden_size
+        if Hkv != H or hd != 64 or H % 4 != 0 or D % 512 != 0:
+            raise ValueError(f"HipEngine needs n_kv == n_heads, head_dim 64, heads % 4 == 0, hidden % 512 == 0 "
+                             f"(got H={H}, Hkv={Hkv}, hd={hd}, D={D})")
+        self._model = model
+        self._device = dev
+        self._dtype = dtype
+        self._max_seq_len = int(max_seq_len)
+        self._batch_size = B = max(1, int(batch_size))
+        self._page_size = PAGE_SIZE
+        self._num_layers = L = cfg.num_hidden_layers
+        self._num_heads = H
+        self._hidden = D
+        self._attn_target = int(attn_target_items)
+
+        # ---- weights: fused / re-laid-out copies (engines/flashinfer.py:152-187) ----
+        self._w: List[Dict[str, Tensor]] = []
+        with torch.no_grad():
+            for lyr in tf.layers:
+                a, mlp = lyr.self_attn, lyr.mlp
+                wqkv = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).to(dtype).contiguous()
+                wgu = kernels.interleave_gate_up(mlp.gate_proj.weight.to(dtype), mlp.up_proj.weight.to(dtype))
+                self._w.append(dict(
+                    wqkv=wqkv, wo=a.o_proj.weight.to(dtype).contiguous(), wgu=wgu,
+                    wd=mlp.down_proj.weight.to(dtype).contiguous(),
+                    ln_in=lyr.input_layernorm.weight.to(dtype).contiguous(),
+                    ln_post=lyr.post_attention_layernorm.weight.to(dtype).contiguous(),
+                    eps_in=float(lyr.input_layernorm.variance_epsilon),
+                    eps_post=float(lyr.post_attention_layernorm.variance_epsilon)))
+            self._final_norm = tf.norm.weight.to(dtype).contiguous()
+            self._final_eps = float(tf.norm.variance_epsilon)
+            self._ffn = self._w[0]["wd"].shape[1]
+            # RoPE table from the model's own rotary embedding (handles llama3
+            # scaling; engines/flashinfer.py:195-255), values of the model dtype.
+            dummy = torch.zeros(1, 1, D, device=dev, dtype=dtype)
+            cos, sin = tf.rotary_emb(dummy, torch.arange(self._max_seq_len, device=dev).unsqueeze(0))
+            self._cos = cos[0].float().contiguous()
+            self._sin = sin[0].float().contiguous()
+
+        # ---- paged KV ----
+        self._pages_per_row = math.ceil(self._max_seq_len / PAGE_SIZE)
+        self._kv = PagedKV(n_layers=L, n_rows=B, pages_per_row=self._pages_per_row, n_heads=H, device=dev,
+                           shuffle_seed=page_table_seed)
+        self._cache_lens: List[int] = [0] * B
+        self._prefix_lens: List[int] = [0] * B
+
+        # ---- native model descriptor ----
+        self._c_layers = (kernels.T3Layer * L)()
+        for li, w in enumerate(self._w):
+            self._c_layers[li] = kernels.T3Layer(
+                w["wqkv"].data_ptr(), w["wo"].data_ptr(), w["wgu"].data_ptr(), w["wd"].data_ptr(),
+                w["ln_in"].data_ptr(), w["ln_post"].data_ptr(), w["eps_in"], w["eps_post"],
+                self._kv.pools[li].data_ptr())
+        self._c_model = kernels.T3Model(
+            L, D, H, self._ffn, ctypes.cast(self._c_layers, ctypes.POINTER(kernels.T3Layer)),
+            self._final_norm.data_ptr(), self._final_eps, self._cos.data_ptr(), self._sin.data_ptr(),
+            self._cos.shape[0], self._kv.n_pages, self._kv.table.data_ptr(), self._kv.table.stride(0),
+            self._kv.table.shape[1])
+
+        self._bufs: Dict[Tuple[int, int], _Buffers] = {}
+        self._plans: Dict[Tuple, AttnPlan] = {}
+
+        # ---- graph state ----
+        self._use_cuda_graph = False
+        self._graph = None
+        self._g_bl = 0
+        self._g_plan: Optional[_GraphPlan] = None
+        self._g_cs_key = None
+        self._head_w: Optional[Tensor] = None
+        self._g_shift_ctx: Optional[Tensor] = None
+        self._g_logits_buf: Optional[Tensor] = None
+        self._g_logits: Optional[Tensor] = None
+        logger.info("HipEngine: layers=%d heads=%d dim=%d batch=%d max_seq=%d pages/row=%d KV=%.2f GiB",
+                    L, H, D, B, self._max_seq_len, self._pages_per_row,
+                    L * self._kv.bytes_per_layer / 2 ** 30)
+
+    # ------------------------------------------------------------------ #
+    #  Introspection / lifecycle (engines/base.py:46-67)
+    # ------------------------------------------------------------------ #
+
+    @property
+    def batch_size(self) -> int:
+        return self._batch_size
+
+    @property
+    def cache_len(self) -> int:
+        return self._cache_lens[0]
+
+    @cache_len.setter
+    def cache_len(self, value: int) -> None:
+        self._cache_lens = [int(value)] * self._batch_size
+
+    @property
+    def cache_lens(self) -> List[int]:
+        return self._cache_lens
+
+    @property
+    def prefix_lens(self) -> List[int]:
+        return self._prefix_lens
+
+    @property
+    def has_cuda_graph(self) -> bool:
+        return self._use_cuda_graph
+
+    @property
+    def kv(self) -> PagedKV:
+        return self._kv
+
+    def reset(self) -> None:
+        self._cache_lens = [0] * self._batch_size
+        self._prefix_lens = [0] * self._batch_size
+        self._g_cs_key = None
+
+    def can_reuse(self, max_seq_len: int, dtype: torch.dtype, *, batch_size: int = 1, page_size: int = 16) -> bool:
+        return (self._max_seq_len >= max_seq_len and self._dtype == dtype
+                and self._batch_size == max(1, batch_size) and self._page_size == page_size)
+
+    def advance_cache(self, block_len: int) -> None:
+        for bi in range(self._batch_size):
+            self._cache_lens[bi] += int(block_len)
+
+    # ------------------------------------------------------------------ #
+    #  Native forward
+    # ------------------------------------------------------------------ #
+
+    def _buffers(self, rows: int, bl: int) -> _Buffers:
+        key = (rows, bl)
+        if key not in self._bufs:
+            self._bufs[key] = _Buffers(rows, bl, self._hidden, self._num_heads, self._ffn, self._device)
+        return self._bufs[key]
+
+    def _plan(self, kv_len: List[int], bl: int) -> AttnPlan:
+        key = (tuple(kv_len), bl)
+        plan = self._plans.get(key)
+        if plan is None:
+            if len(self._plans) > 64:
+                self._plans.clear()
+            plan = AttnPlan(kv_len, bl, self._num_heads, self._device, target_items=self._attn_target)
+            self._plans[key] = plan
+        return plan
+
+    def _starts(self, cache_starts: CacheStarts, rows: int) -> List[int]:
+        starts = [int(cache_starts)] * rows if isinstance(cache_starts, int) else [int(c) for c in cache_starts]
+        if len(starts) != rows:
+            raise ValueError(f"cache_starts has {len(starts)} entries for {rows} rows")
+        return starts
+
+    def _check_capacity(self, starts: List[int], bl: int) -> None:
+        if max(starts) + bl > min(self._max_seq_len, self._pages_per_row * PAGE_SIZE):
+            raise ValueError(f"block [{max(starts)}, {max(starts) + bl}) exceeds max_seq_len {self._max_seq_len}")
+        if min(starts) < 0:
+            raise ValueError("negative cache start")
+
+    def _workspace(self, buf: _Buffers, plan: "AttnPlan | _GraphPlan") -> kernels.T3Workspace:
+        return kernels.T3Workspace(
+            buf.residual.data_ptr(), buf.q.data_ptr(), buf.attn.data_ptr(), buf.normed.data_ptr(),
+            buf.delta.data_ptr(), buf.act.data_ptr(), plan.work.data_ptr(), int(plan.work.shape[0]),
+            kernels.ptr(plan.merge), 0 if plan.merge is None else int(plan.merge.shape[0]),
+            kernels.ptr(getattr(plan, "counts", None)), kernels.ptr(plan.part_o), kernels.ptr(plan.part_ml),
+            int(plan.n_slots))
+
+    def _run(self, buf: _Buffers, plan, kv_len_dev: Tensor, *, causal: bool = False,
+             head_w: Optional[Tensor] = None, shift_ctx: Optional[Tensor] = None,
+             logits: Optional[Tensor] = None) -> None:
+        ws = self._workspace(buf, plan)
+        V = 0 if head_w is None else int(head_w.shape[0])
+        kernels.check(kernels.load_library().yapd_t3_block_forward(
+            ctypes.byref(self._c_model), ctypes.byref(ws), buf.emb.data_ptr(), buf.rows, buf.bl,
+            buf.pos0.data_ptr(), kv_len_dev.data_ptr(), int(causal), buf.hidden.data_ptr(),
+            kernels.ptr(head_w), V, kernels.ptr(shift_ctx), kernels.ptr(logits),
+            0 if logits is None else logits.stride(1), kernels.stream_ptr(self._device)))
+
+    # ------------------------------------------------------------------ #
+    #  Prefix forward (engines/base.py:71-83)
+    # ------------------------------------------------------------------ #
+
+    def prefix_forward(self, prefix_emb_or_list: Union[Tensor, List[Tensor]]) -> Tensor:
+        """Prefill each row's prefix causally; returns the SOS hidden ``(B, 1, D)``."""
+        B = self._batch_size
+        D = self._hidden
+        if isinstance(prefix_emb_or_list, list):
+            embs = [e.reshape(-1, D) for e in prefix_emb_or_list]
+            if len(embs) == 1 and B > 1:
+                embs = embs * B
+            if len(embs) != B:
+                raise ValueError(f"prefix list length {len(embs)} != engine batch {B}")
+        else:
+            t = prefix_emb_or_list
+            if t.size(0) not in (1, B):
+                raise ValueError(f"prefix batch {t.size(0)} must be 1 or engine batch {B}")
+            embs = [t[min(i, t.size(0) - 1)] for i in range(B)]
+        lps = [int(e.shape[0]) for e in embs]
+        if max(lps) > self._max_seq_len:
+            raise ValueError("prefix longer than max_seq_len")
+        lp_max = max(lps)
+        sos = torch.empty(B, 1, D, dtype=self._dtype, device=self._device)
+        done = [False] * B
+        for c0 in range(0, lp_max, PREFILL_CHUNK):
+            bl = min(PREFILL_CHUNK, lp_max - c0)
+            buf = self._buffers(B, bl)
+            buf.emb.zero_()
+            for r, e in enumerate(embs):
+                n = max(0, min(bl, lps[r] - c0))
+                if n > 0:
+                    buf.emb[r * bl: r * bl + n].copy_(e[c0: c0 + n].to(self._dtype))
+            buf.pos0.fill_(c0)
+            kv_len = [c0 + bl] * B
+            plan = self._plan(kv_len, bl)
+            self._run(buf, plan, plan.kv_len, causal=True)
+            hid = buf.hidden.view(B, bl, D)
+            for r in range(B):
+                if not done[r] and c0 <= lps[r] - 1 < c0 + bl:
+                    sos[r, 0] = hid[r, lps[r] - 1 - c0]
+                    done[r] = True
+        self._cache_lens = list(lps)
+        self._prefix_lens = list(lps)
+        return sos
+
+    # ------------------------------------------------------------------ #
+    #  Block forward (engines/base.py:85-98)
+    # ------------------------------------------------------------------ #
+
+    def block_forward(self, block_emb: Tensor, cache_starts: CacheStarts) -> Tensor:
+        """Eager block forward; writes the block KV tentatively at ``[cs, cs+bl)``."""
+        B, bl, D = block_emb.shape
+        if B != self._batch_size or D != self._hidden:
+            raise ValueError(f"block_emb must be ({self._batch_size}, bl, {self._hidden}); got {tuple(block_emb.shape)}")
+        if not 1 <= bl <= 64:
+            raise ValueError("block length must be in [1, 64]")
+        starts = self._starts(cache_starts, B)
+        self._check_capacity(starts, bl)
+        buf = self._buffers(B, bl)
+        buf.emb.copy_(block_emb.reshape(B * bl, D))
+        buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+        plan = self._plan([s + bl for s in starts], bl)
+        self._run(buf, plan, plan.kv_len)
+        return buf.hidden.view(B, bl, D).clone()
+
+    # ------------------------------------------------------------------ #
+    #  Graph path (engines/base.py:100-113, 119-141)
+    # ------------------------------------------------------------------ #
+
+    def set_shift_ctx(self, ctx: Tensor) -> None:
+        if self._g_shift_ctx is not None:
+            if ctx.size(0) < self._batch_size:
+                self._g_shift_ctx.copy_(ctx.expand(self._batch_size, -1, -1))
+            else:
+                self._g_shift_ctx.copy_(ctx)
+
+    def capture_cuda_graph(self, block_size: int, *, speech_head: Optional[torch.nn.Linear] = None) -> None:
+        if self._use_cuda_graph and self._g_bl == block_size:
+            return
+        B, bl, D = self._batch_size, int(block_size), self._hidden
+        buf = self._buffers(B, bl)
+        self._g_bl = bl
+        self._g_plan = _GraphPlan(B, bl, self._num_heads, self._device, self._attn_target)
+        starts = [min(c, self._max_seq_len - bl) for c in self._cache_lens]
+        self._update_graph_inputs(starts)
+        if speech_head is not None:
+            self._head_w = speech_head.weight.detach().to(self._dtype).contiguous()
+            if speech_head.bias is not None:
+                raise ValueError("HipEngine folds a bias-free speech head (T3 speech_head has no bias)")
+            V = self._head_w.shape[0]
+            pitch = (V + 7) // 8 * 8  # 16-byte aligned rows
+            self._g_shift_ctx = torch.zeros(B, 1, D, dtype=self._dtype, device=self._device)
+            self._g_logits_buf = torch.zeros(B, bl, pitch, dtype=self._dtype, device=self._device)
+            self._g_logits = self._g_logits_buf[..., :V]
+        body = lambda: self._run(buf, self._g_plan, self._g_plan.kv_len, head_w=self._head_w,
+                                 shift_ctx=self._g_shift_ctx, logits=self._g_logits)
+        body()  # warm-up outside the graph
+        torch.cuda.synchronize(self._device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            body()
+        self._graph = graph
+        self._use_cuda_graph = True
+        logger.info("HipEngine: graph captured (block=%d, batch=%d, head=%s)", bl, B, self._head_w is not None)
+
+    def _update_graph_inputs(self, starts: List[int]) -> None:
+        key = tuple(starts)
+        if key == self._g_cs_key:
+            return
+        bl = self._g_bl
+        self._check_capacity(starts, bl)
+        buf = self._buffers(self._batch_size, bl)
+        buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+        self._g_plan.update([s + bl for s in starts])
+        self._g_cs_key = key
+
+    def block_forward_graph(self, block_emb: Tensor, cache_starts: CacheStarts) -> Tuple[Tensor, Optional[Tensor]]:
+        bl = block_emb.size(1)
+        if not self._use_cuda_graph or bl != self._g_bl:
+            return self.block_forward(block_emb, cache_starts), None
+        B, D = self._batch_size, self._hidden
+        buf = self._buffers(B, bl)
+        buf.emb.copy_(block_emb.reshape(B * bl, D))
+        self._update_graph_inputs(self._starts(cache_starts, B))
+        self._graph.replay()
+        return buf.hidden.view(B, bl, D), self._g_logits
+
+
+class _GraphPlan:
+    """Attention plan with fixed-capacity device buffers, refreshed in place.
+
+    The captured grid is sized by the capacity; the kernels read the live
+    item counts from ``counts``.
+    """
+
+    def __init__(self, rows: int, bl: int, n_heads: int, device: torch.device, target_items: int):
+        self.rows, self.bl, self.target = rows, bl, target_items
+        cap_items = rows + target_items
+        self.work = torch.zeros(cap_items, 4, dtype=torch.int32, device=device)
+        self.merge = torch.zeros(rows, 3, dtype=torch.int32, device=device)
+        self.counts = torch.zeros(2, dtype=torch.int32, device=device)
+        self.kv_len = torch.ones(rows, dtype=torch.int32, device=device)
+        self.n_slots = cap_items
+        self.part_o = torch.empty(cap_items, bl, n_heads, 64, dtype=torch.float32, device=device)
+        self.part_ml = torch.empty(cap_items, bl, n_heads, 2, dtype=torch.float32, device=device)
+        self.update([bl] * rows)
+
+    def update(self, kv_len: List[int]) -> None:
+        work, merge, n_slots = kernels.attn_plan(kv_len, target_items=self.target)
+        if work.shape[0] > self.work.shape[0] or n_slots > self.n_slots:
+            raise RuntimeError("attention plan exceeds the captured capacity")
+        self.work[: work.shape[0]].copy_(torch.from_numpy(work))
+        if merge.shape[0]:
+            self.merge[: merge.shape[0]].copy_(torch.from_numpy(merge))
+        self.counts.copy_(torch.tensor([work.shape[0], merge.shape[0]], dtype=torch.int32))
+        self.kv_len.copy_(torch.tensor(kv_len, dtype=torch.int32))

@@ -35,11 +35,42 @@ _SIGNATURES = {
     "yapd_attn_plan": (c_int, [c_void, c_int, c_int, c_int, c_void, c_int, c_void, c_int, c_void, c_void, c_void]),
     "yapd_attn_paged_block": (c_int, [
         c_void, c_void, c_i64, c_void, c_int, c_int, c_void, c_int, c_int, c_int, c_void, c_int, c_void, c_int,
-        c_void, c_void, c_int, c_float, c_void, c_void]),
+        c_void, c_void, c_void, c_int, c_float, c_int, c_void, c_void]),
     "yapd_kv_write": (c_int, [c_void, c_void, c_i64, c_i64, c_void, c_i64, c_void, c_int, c_int, c_void, c_int,
                               c_int, c_int, c_void]),
     "yapd_kv_gather": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_void]),
+    "yapd_gemm_bf16": (c_int, [c_void, c_i64, c_void, c_i64, c_int, c_int, c_int, c_void, c_i64, c_void]),
+    "yapd_gemm_head_shift": (c_int, [c_void, c_void, c_int, c_int, c_int, c_void, c_i64, c_int, c_void, c_i64,
+                                     c_void]),
+    "yapd_gemm_swiglu": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_i64, c_void]),
+    "yapd_gemm_qkv_rope_kv": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_int, c_void,
+                                      c_int, c_void, c_void, c_i64, c_void, c_int, c_int, c_void]),
+    "yapd_rmsnorm": (c_int, [c_void, c_void, c_void, c_void, c_float, c_int, c_int, c_void, c_void]),
+    "yapd_t3_block_forward": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void, c_int, c_void,
+                                      c_void, c_int, c_void, c_void, c_i64, c_void]),
 }
+
+
+class T3Layer(ctypes.Structure):
+    """``yapd_t3_layer`` of include/yapd_t3.h."""
+    _fields_ = [("w_qkv", c_void), ("w_o", c_void), ("w_gate_up", c_void), ("w_down", c_void),
+                ("ln_in", c_void), ("ln_post", c_void), ("eps_in", c_float), ("eps_post", c_float),
+                ("kv_pool", c_void)]
+
+
+class T3Model(ctypes.Structure):
+    """``yapd_t3_model`` of include/yapd_t3.h."""
+    _fields_ = [("n_layers", c_int), ("hidden", c_int), ("n_heads", c_int), ("ffn", c_int),
+                ("layers", ctypes.POINTER(T3Layer)), ("final_norm", c_void), ("final_eps", c_float),
+                ("rope_cos", c_void), ("rope_sin", c_void), ("rope_positions", c_int), ("n_pages", c_i64),
+                ("page_table", c_void), ("table_stride", c_int), ("table_cols", c_int)]
+
+
+class T3Workspace(ctypes.Structure):
+    """``yapd_t3_workspace`` of include/yapd_t3.h."""
+    _fields_ = [("residual", c_void), ("q", c_void), ("attn", c_void), ("normed", c_void), ("delta", c_void),
+                ("act", c_void), ("work", c_void), ("n_work", c_int), ("merge", c_void), ("n_merge", c_int),
+                ("counts", c_void), ("part_o", c_void), ("part_ml", c_void), ("n_slots", c_int)]
 
 
 class HipKernelError(RuntimeError):
@@ -153,11 +184,13 @@ def score_cfg_pmi_unmask(
 # (a) paged block attention
 # --------------------------------------------------------------------------- #
 
-def attn_plan(kv_len, target_items: int = 1024, min_split_keys: int = 128):
+def attn_plan(kv_len, target_items: int = 192, min_split_keys: int = 128):
     """Host planner: ``(work [n,4] int32, merge [m,3] int32, n_slots)`` numpy arrays.
 
     Rows are cut into work items of whole 32-key chunks so that about
-    ``target_items`` items exist; items are ordered longest first.
+    ``target_items`` items exist (192 is roughly how many four-head work items
+    the MI355X keeps in flight, so only rows longer than the average share are
+    split); items are ordered longest first.
     """
     import numpy as np
     kv = np.ascontiguousarray(np.asarray(kv_len, dtype=np.int32))
@@ -175,8 +208,12 @@ def attn_plan(kv_len, target_items: int = 1024, min_split_keys: int = 128):
 
 def attn_paged_block(q: torch.Tensor, pool: torch.Tensor, table: torch.Tensor, kv_len: torch.Tensor,
                      work: torch.Tensor, merge: Optional[torch.Tensor], part_o: Optional[torch.Tensor],
-                     part_ml: Optional[torch.Tensor], out: torch.Tensor, scale: float) -> None:
-    """``out [rows, bl, H, 64] = softmax(q K^T * scale) V`` over each row's pages."""
+                     part_ml: Optional[torch.Tensor], out: torch.Tensor, scale: float,
+                     causal: bool = False) -> None:
+    """``out [rows, bl, H, 64] = softmax(q K^T * scale) V`` over each row's pages.
+
+    ``causal``: query ``i`` of the block sees keys ``< kv_len - bl + i + 1`` (prefill).
+    """
     dev = q.device
     require_cuda(q, "q", torch.bfloat16, dev)
     require(q.dim() == 4 and q.shape[3] == 64, "q must be [rows, bl, H, 64]")
@@ -205,8 +242,8 @@ def attn_paged_block(q: torch.Tensor, pool: torch.Tensor, table: torch.Tensor, k
     check(load_library().yapd_attn_paged_block(
         q.data_ptr(), pool.data_ptr(), pool.shape[0], table.data_ptr(), table.stride(0), table.shape[1],
         kv_len.data_ptr(),
-        rows, bl, H, work.data_ptr(), int(work.shape[0]), ptr(merge), n_merge, ptr(part_o), ptr(part_ml),
-        n_slots, float(scale), out.data_ptr(), stream_ptr(dev)))
+        rows, bl, H, work.data_ptr(), int(work.shape[0]), ptr(merge), n_merge, None, ptr(part_o), ptr(part_ml),
+        n_slots, float(scale), int(bool(causal)), out.data_ptr(), stream_ptr(dev)))
 
 
 def kv_write(k: torch.Tensor, v: torch.Tensor, pool: torch.Tensor, table: torch.Tensor,
@@ -241,3 +278,109 @@ def kv_gather(pool: torch.Tensor, table_row: torch.Tensor, kv_len: int):
     check(load_library().yapd_kv_gather(pool.data_ptr(), pool.shape[0], table_row.data_ptr(), table_row.numel(),
                                         int(kv_len), H, k.data_ptr(), v.data_ptr(), stream_ptr(dev)))
     return k, v
+
+
+# --------------------------------------------------------------------------- #
+# (b) GEMMs and norms
+# --------------------------------------------------------------------------- #
+
+def _mat(t: torch.Tensor, name: str, dev) -> None:
+    require_cuda(t, name, torch.bfloat16, dev, contiguous=False)
+    require(t.dim() == 2 and t.stride(1) == 1, f"{name} must be a 2-D row-major view")
+
+
+def gemm_bf16(A: torch.Tensor, W: torch.Tensor, out: torch.Tensor) -> None:
+    """``out[M, N] = A[M, K] @ W[N, K]^T`` in bf16 with fp32 accumulation."""
+    dev = A.device
+    _mat(A, "A", dev)
+    _mat(W, "W", dev)
+    _mat(out, "out", dev)
+    M, K = A.shape
+    N = W.shape[0]
+    require(W.shape[1] == K and tuple(out.shape) == (M, N), "gemm shapes")
+    check(load_library().yapd_gemm_bf16(A.data_ptr(), A.stride(0), W.data_ptr(), W.stride(0), M, N, K,
+                                        out.data_ptr(), out.stride(0), stream_ptr(dev)))
+
+
+def gemm_head_shift(hidden: torch.Tensor, shift_ctx: torch.Tensor, W: torch.Tensor, logits: torch.Tensor) -> None:
+    """Token-shifted head: ``logits[r, j] = W @ (j ? hidden[r, j-1] : shift_ctx[r])``.
+
+    ``hidden [rows, bl, D]`` contiguous, ``shift_ctx [rows, 1, D]`` contiguous,
+    ``logits [rows, bl, V]`` with a unit last stride (padded pitch allowed).
+    """
+    dev = hidden.device
+    require_cuda(hidden, "hidden", torch.bfloat16, dev)
+    require_cuda(shift_ctx, "shift_ctx", torch.bfloat16, dev)
+    _mat(W, "W", dev)
+    rows, bl, D = hidden.shape
+    require(tuple(shift_ctx.shape) == (rows, 1, D), "shift_ctx must be [rows, 1, D]")
+    require_cuda(logits, "logits", torch.bfloat16, dev, contiguous=False)
+    V = W.shape[0]
+    require(tuple(logits.shape) == (rows, bl, V) and logits.stride(2) == 1 and logits.stride(0) == bl * logits.stride(1),
+            "logits must be [rows, bl, V] with rows packed")
+    check(load_library().yapd_gemm_head_shift(hidden.data_ptr(), shift_ctx.data_ptr(), rows, bl, D, W.data_ptr(),
+                                              W.stride(0), V, logits.data_ptr(), logits.stride(1), stream_ptr(dev)))
+
+
+def gemm_swiglu(A: torch.Tensor, W_gu_interleaved: torch.Tensor, act: torch.Tensor) -> None:
+    """``act[M, F] = silu(A Wg^T) * (A Wu^T)`` with gate/up rows interleaved per 32 (see interleave_gate_up)."""
+    dev = A.device
+    _mat(A, "A", dev)
+    require_cuda(W_gu_interleaved, "W_gu", torch.bfloat16, dev)
+    _mat(act, "act", dev)
+    M, K = A.shape
+    F = W_gu_interleaved.shape[0] // 2
+    require(W_gu_interleaved.shape[1] == K and tuple(act.shape) == (M, F), "swiglu shapes")
+    check(load_library().yapd_gemm_swiglu(A.data_ptr(), A.stride(0), W_gu_interleaved.data_ptr(), M, F, K,
+                                          act.data_ptr(), act.stride(0), stream_ptr(dev)))
+
+
+def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """Rows ``[g(32w..32w+31); u(32w..32w+31)]`` for w = 0..F/32-1: gate and up of a
+    feature land in the same lane of the swiglu epilogue."""
+    F, K = w_gate.shape
+    require(F % 64 == 0 and w_up.shape == w_gate.shape, "gate/up must be [F, K] with F % 64 == 0")
+    return torch.stack([w_gate.view(F // 32, 32, K), w_up.view(F // 32, 32, K)], 1).reshape(2 * F, K).contiguous()
+
+
+def gemm_qkv_rope_kv(A: torch.Tensor, W_qkv: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor,
+                     pos0: torch.Tensor, bl: int, q_out: torch.Tensor, pool: torch.Tensor,
+                     table: torch.Tensor) -> None:
+    """Fused QKV projection + NeoX RoPE + paged KV write (q to ``q_out [M, H*64]``)."""
+    dev = A.device
+    _mat(A, "A", dev)
+    require_cuda(W_qkv, "W_qkv", torch.bfloat16, dev)
+    M, K = A.shape
+    H = pool.shape[2]
+    require(tuple(W_qkv.shape) == (3 * H * 64, K), "W_qkv must be [3*H*64, K]")
+    require_cuda(cos_t, "cos_t", torch.float32, dev)
+    require_cuda(sin_t, "sin_t", torch.float32, dev)
+    require(cos_t.shape == sin_t.shape and cos_t.dim() == 2 and cos_t.shape[1] == 64, "cos/sin must be [P, 64]")
+    require_cuda(pos0, "pos0", torch.int32, dev)
+    require(M % bl == 0 and pos0.numel() == M // bl, "pos0 must have M / bl entries")
+    require_cuda(q_out, "q_out", torch.bfloat16, dev)
+    require(tuple(q_out.shape) in ((M, H * 64), (M // bl, bl, H, 64)), "q_out shape")
+    require_cuda(pool, "pool", torch.bfloat16, dev)
+    require_cuda(table, "table", torch.int32, dev, contiguous=False)
+    require(table.stride(1) == 1 and table.shape[0] >= M // bl, "table shape")
+    check(load_library().yapd_gemm_qkv_rope_kv(
+        A.data_ptr(), A.stride(0), W_qkv.data_ptr(), M, K, H, cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0],
+        pos0.data_ptr(), bl, q_out.data_ptr(), pool.data_ptr(), pool.shape[0], table.data_ptr(), table.stride(0),
+        table.shape[1], stream_ptr(dev)))
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor,
+            delta: Optional[torch.Tensor] = None) -> None:
+    """``out = rmsnorm(x) * w``; with ``delta``: ``x += delta`` (bf16, in place) first."""
+    dev = x.device
+    for name, t in (("x", x), ("w", w), ("out", out)):
+        require_cuda(t, name, torch.bfloat16, dev)
+    D = x.shape[-1]
+    M = x.numel() // D
+    require(out.shape == x.shape and w.numel() == D, "rmsnorm shapes")
+    if delta is not None:
+        require_cuda(delta, "delta", torch.bfloat16, dev)
+        require(delta.shape == x.shape, "delta shape")
+    check(load_library().yapd_rmsnorm(ptr(delta), x.data_ptr() if delta is not None else None,
+                                      x.data_ptr() if delta is None else None, w.data_ptr(), float(eps), M, D,
+                                      out.data_ptr(), stream_ptr(dev)))

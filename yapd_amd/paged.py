@@ -63,7 +63,7 @@ class AttnPlan:
     """Device work list + split-KV workspace for one set of per-row kv lengths."""
 
     def __init__(self, kv_len: Sequence[int], bl: int, n_heads: int, device: torch.device,
-                 target_items: int = 1024, min_split_keys: int = 128):
+                 target_items: int = 192, min_split_keys: int = 128):
         work, merge, n_slots = kernels.attn_plan(kv_len, target_items=target_items, min_split_keys=min_split_keys)
         self.kv_len_host = [int(x) for x in kv_len]
         self.work = torch.from_numpy(work).to(device)
@@ -77,8 +77,8 @@ class AttnPlan:
             self.part_o = self.part_ml = None
 
     def run(self, q: torch.Tensor, pool: torch.Tensor, table: torch.Tensor, out: torch.Tensor,
-            scale: float) -> None:
+            scale: float, causal: bool = False) -> None:
         kernels.require(max(self.kv_len_host) <= table.shape[1] * PAGE_SIZE,
                         "page table maps fewer positions than kv_len")
         kernels.attn_paged_block(q, pool, table, self.kv_len, self.work, self.merge, self.part_o, self.part_ml,
-                                 out, scale)
+                                 out, scale, causal=causal)

@@ -97,3 +97,84 @@ def log_uniform_lengths(n: int, lo: int, hi: int, seed: int) -> List[int]:
     g = torch.Generator().manual_seed(seed)
     u = torch.rand(n, generator=g, dtype=torch.float64)
     return [int(round(math.exp(math.log(lo) + float(x) * (math.log(hi) - math.log(lo))))) for x in u]
+
+
+# --------------------------------------------------------------------------- #
+# Synthetic T3 backbone
+# --------------------------------------------------------------------------- #
+
+class SyntheticT3(torch.nn.Module):
+    """T3-shaped model: ``tfmr`` (a transformers ``LlamaModel``), ``speech_head``
+    (bias-free Linear D -> V) and ``speech_emb`` (V + 1 rows: the extra row is
+    MASK, chatterbox_flash/model.py:340-352)."""
+
+    def __init__(self, tfmr, speech_head, speech_emb):
+        super().__init__()
+        self.tfmr = tfmr
+        self.speech_head = speech_head
+        self.speech_emb = speech_emb
+
+    @property
+    def device(self) -> torch.device:
+        return self.tfmr.norm.weight.device
+
+    def embed_speech_tokens(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Speech-token embedding lookup (chatterbox_flash/model.py:397-402 without
+        the learned position embedding, which this synthetic model omits)."""
+        return self.speech_emb(tokens)
+
+
+def make_t3(*, n_layers: int = 30, hidden: int = 1024, heads: int = 16, ffn: int = 4096,
+            vocab: int = SPEECH_VOCAB, rope_theta: float = 10000.0, rope_parameters: Optional[dict] = None,
+            eps: float = 1e-5, max_positions: int = 8192, seed: int = 0, dtype=torch.bfloat16, device="cpu",
+            norm_jitter: bool = False, weight_std: float = 0.02) -> SyntheticT3:
+    """Random-init T3 backbone with a fixed draw order.
+
+    Per layer, in order: q, k, v, o, gate, up, down ~ N(0, weight_std); then
+    (if ``norm_jitter``) input/post-attention RMSNorm gains ~ U(0.5, 1.5),
+    else 1 (HF init).  Then the final-norm gain (same rule), speech head
+    ~ N(0, weight_std) and speech embeddings ~ N(0, 1).
+    """
+    from transformers import LlamaConfig, LlamaModel
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    kw = dict(hidden_size=hidden, intermediate_size=ffn, num_hidden_layers=n_layers, num_attention_heads=heads,
+              num_key_value_heads=heads, head_dim=hidden // heads, rms_norm_eps=eps, vocab_size=8,
+              max_position_embeddings=max_positions, attn_implementation="sdpa")
+    if rope_parameters is None:
+        kw["rope_theta"] = rope_theta
+    else:
+        kw["rope_parameters"] = dict(rope_parameters)
+    cfg = LlamaConfig(**kw)
+    with torch.device("meta"):
+        tf = LlamaModel(cfg)
+    tf = tf.to_empty(device=device).to(dtype)
+    g = torch.Generator().manual_seed(seed)
+
+    def normal(shape, std):
+        return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+    def gain(n):
+        return (torch.rand(n, generator=g) + 0.5).to(dtype) if norm_jitter else torch.ones(n, dtype=dtype)
+
+    hd = hidden // heads
+    with torch.no_grad():
+        for lyr in tf.layers:
+            a, m = lyr.self_attn, lyr.mlp
+            a.q_proj.weight.copy_(normal((heads * hd, hidden), weight_std))
+            a.k_proj.weight.copy_(normal((heads * hd, hidden), weight_std))
+            a.v_proj.weight.copy_(normal((heads * hd, hidden), weight_std))
+            a.o_proj.weight.copy_(normal((hidden, heads * hd), weight_std))
+            m.gate_proj.weight.copy_(normal((ffn, hidden), weight_std))
+            m.up_proj.weight.copy_(normal((ffn, hidden), weight_std))
+            m.down_proj.weight.copy_(normal((hidden, ffn), weight_std))
+            lyr.input_layernorm.weight.copy_(gain(hidden))
+            lyr.post_attention_layernorm.weight.copy_(gain(hidden))
+        tf.norm.weight.copy_(gain(hidden))
+        tf.embed_tokens.weight.zero_()
+        tf.rotary_emb = LlamaRotaryEmbedding(config=cfg).to(device)  # fp32 inv_freq
+        head = torch.nn.Linear(hidden, vocab, bias=False, device=device, dtype=dtype)
+        head.weight.copy_(normal((vocab, hidden), weight_std))
+        emb = torch.nn.Embedding(vocab + 1, hidden, device=device, dtype=dtype)
+        emb.weight.copy_(normal((vocab + 1, hidden), 1.0))
+    return SyntheticT3(tf, head, emb).eval()
