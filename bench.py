@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark: the full 30-layer T3 block-diffusion decode step on one MI355X.
+
+Workload (synthetic, seeded): 256 CFG pairs = 512 rows in generate()'s
+stacked order, block 32, prefix lengths U[150, 600] per pair (both rows of a
+pair share it), prefixes prefilled through the engine, shuffled page table,
+30-layer Llama (hidden 1024, 16 x 64 heads, FFN 4096, RMSNorm eps 1e-5, RoPE
+theta 10000, linear weights N(0, 0.02)), speech head V = 8194, then CFG
+(w = 0.5) + PMI (Dirichlet(0.1) prior) + time-shifted-quantile unmask
+(tau = 3.0, K = 10, t_shift 0.5).  One step = embedding -> backbone -> head ->
+scoring, replayed as one HIP graph.
+
+Prints one JSON line.  ``value`` = speech tokens/s = pairs * block / step time.
+``roofline`` describes the dominant kernel (the gate/up + SiLU GEMM);
+``kernels`` adds attention and scoring against the HBM roofline.  Per-kernel
+durations come from HIP events around single launches on the stream the
+kernel runs on, right after the timed region.  ``cpu_baseline`` times the
+oracle (torch on the host cores) on a bounded sample of the same step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--pairs", type=int, default=256)
+    ap.add_argument("--block", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(fn, reps, dev):
+    """Average device time of ``fn`` (one or more launches) over ``reps`` with stream events."""
+    s = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    fn()
+    for i in range(reps):
+        starts[i].record(s)
+        fn()
+        ends[i].record(s)
+    torch.cuda.synchronize(dev)
+    return sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / reps  # ms
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU (data-parallel over pairs) is not "
+                                   "part of it", "n_gpus": args.gpus}))
+        sys.exit(2)
+    from yapd_amd import kernels
+    from yapd_amd.engines.hip import HipEngine
+    from yapd_amd.paged import AttnPlan
+    from yapd_amd.step import DecodeStep
+    from yapd_amd.synthetic import MASK_ID, STOP_ID, make_t3, scoring_inputs, uniform_lengths
+
+    kernels.load_library()
+    dev = torch.device("cuda:0")
+    Bp, bl, L = args.pairs, args.block, args.layers
+    B = 2 * Bp
+    D, H, F, V = 1024, 16, 4096, 8194
+    t0 = time.time()
+    model = make_t3(n_layers=L, seed=args.seed, device=dev)
+    lens = uniform_lengths(Bp, 150, 600, seed=args.seed + 1)
+    lps = lens + lens  # stacked rows: cond 0..Bp-1, null Bp..2Bp-1
+    max_seq = max(lps) + 2 * bl
+    eng = HipEngine(model, max_seq, torch.bfloat16, batch_size=B, page_table_seed=args.seed + 2)
+    g = torch.Generator().manual_seed(args.seed + 3)
+    prefixes = [torch.randn(lp, D, generator=g).to(torch.bfloat16) for lp in lens]
+    sos = eng.prefix_forward([p.to(dev) for p in prefixes + prefixes])
+    torch.cuda.synchronize(dev)
+    log(f"model + prefill ready in {time.time() - t0:.1f}s (KV {L * eng.kv.bytes_per_layer / 2**30:.1f} GiB)")
+
+    sc_in = scoring_inputs(n_pairs=Bp, bl=bl, vocab=V, seed=args.seed + 4, layout="stacked")
+    step = DecodeStep(eng, model, n_pairs=Bp, block_size=bl, log_prior=sc_in.log_prior.to(dev), mask_id=MASK_ID,
+                      stop_id=STOP_ID, num_steps=10, time_shift_tau=3.0, omnivoice_t_shift=0.5, cfg_scale=0.5)
+    step.xt.copy_(sc_in.xt.to(dev))
+    step.k_step.copy_(sc_in.k_step.to(dev))
+    step.capture(lps, sos)
+    for _ in range(args.warmup):
+        step.replay()
+    torch.cuda.synchronize(dev)
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    st.record()
+    for _ in range(args.steps):
+        step.replay()
+    en.record()
+    torch.cuda.synchronize(dev)
+    ms = st.elapsed_time(en) / args.steps
+    log(f"step {ms:.3f} ms")
+
+    # ---- per-kernel durations (HIP events around single launches, same stream) ----
+    buf = eng._buffers(B, bl)
+    plan = eng._g_plan
+    N = B * bl
+    w0 = eng._w[0]
+    ms_swiglu = time_launches(lambda: kernels.gemm_swiglu(buf.normed, w0["wgu"], buf.act), 20, dev)
+    ms_qkv = time_launches(lambda: kernels.gemm_qkv_rope_kv(buf.normed, w0["wqkv"], eng._cos, eng._sin, buf.pos0,
+                                                            bl, buf.q, eng.kv.pools[0], eng.kv.table), 20, dev)
+    ms_o = time_launches(lambda: kernels.gemm_bf16(buf.attn, w0["wo"], buf.delta), 20, dev)
+    ms_down = time_launches(lambda: kernels.gemm_bf16(buf.act, w0["wd"], buf.delta), 20, dev)
+    eager_plan = AttnPlan(plan.kv_len.tolist(), bl, H, dev)
+    ms_attn = time_launches(lambda: eager_plan.run(buf.q.view(B, bl, H, 64), eng.kv.pools[0], eng.kv.table,
+                                                   buf.attn.view(B, bl, H, 64), 0.125), 20, dev)
+    # scoring on two rotated logits sets (the 268 MB input must not sit in the 256 MB MALL)
+    sets = [eng._g_logits]
+    spare = torch.empty_like(eng._g_logits_buf)
+    spare.copy_(eng._g_logits_buf)
+    sets.append(spare[..., :V])
+    it = [0]
+
+    def score_once():
+        it[0] ^= 1
+        step.scorer(sets[it[0]], step.xt, step.k_step, layout="stacked")
+    ms_score = time_launches(score_once, 20, dev)
+
+    flops_swiglu = 2.0 * N * (2 * F) * D
+    tf_swiglu = flops_swiglu / (ms_swiglu * 1e-3) / 1e12
+    kv_len = plan.kv_len.tolist()
+    attn_bytes = sum(kv_len) * H * 64 * 2 * 2 + 2 * N * H * 64 * 2 + sum((k + 15) // 16 for k in kv_len) * 4
+    score_bytes = B * bl * V * 2 + V * 4 + Bp * bl * (8 + 8 + 4 + 1 + 8) + Bp * 13
+    gbs_attn = attn_bytes / (ms_attn * 1e-3) / 1e9
+    gbs_score = score_bytes / (ms_score * 1e-3) / 1e9
+    proj_flops = 2.0 * N * D * (3 * H * 64 + H * 64 + 2 * F + F) * L + 2.0 * N * D * V
+    log(f"gate/up {ms_swiglu*1e3:.1f} us ({tf_swiglu:.0f} TF/s), qkv {ms_qkv*1e3:.1f}, o {ms_o*1e3:.1f}, "
+        f"down {ms_down*1e3:.1f}, attn {ms_attn*1e3:.1f} us ({gbs_attn:.0f} GB/s), score {ms_score*1e3:.1f} us "
+        f"({gbs_score:.0f} GB/s)")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_swiglu_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(model, eng, lps, bl, sc_in, args.cpu_layers, L)
+
+    tok_s = Bp * bl / (ms * 1e-3)
+    out = {
+        "metric": "speech tokens/sec, 30-layer T3 step at B=256; attn/score HBM GB/s % peak",
+        "value": round(tok_s, 1),
+        "unit": "speech tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights of the T3 architecture, random prefixes)",
+        "config": {"workload": "T3 block-diffusion decode step: embed + 30-layer backbone + speech head + "
+                               "CFG/PMI/quantile unmask", "pairs": Bp, "rows": B, "block": bl, "layers": L,
+                   "hidden": D, "heads": H, "ffn": F, "vocab": V, "prefix_len": "U[150,600] per pair",
+                   "page_table": "shuffled", "cfg_w": 0.5, "quantile_tau": 3.0, "K": 10},
+        "rows_positions_per_s": round(B * bl / (ms * 1e-3), 1),
+        "projection_tflops": round(proj_flops / (ms * 1e-3) / 1e12, 1),
+        "roofline": {"kernel": "gemm_kernel<swiglu> (gate/up + SiLU*up, M=%d N=%d K=%d)" % (N, 2 * F, D),
+                     "bound": "mfma", "achieved": round(tf_swiglu, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf_swiglu / BF16_PEAK_TFLOPS, 4), "traffic": traffic},
+        "kernels": {
+            "attention": {"us": round(ms_attn * 1e3, 1), "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4)},
+            "scoring": {"us": round(ms_score * 1e3, 1), "achieved": round(gbs_score, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs_score / HBM_PEAK_GBS, 4)},
+            "gemm_us": {"qkv_rope_kv": round(ms_qkv * 1e3, 1), "o_proj": round(ms_o * 1e3, 1),
+                        "gate_up_swiglu": round(ms_swiglu * 1e3, 1), "down": round(ms_down * 1e3, 1)},
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(model, eng, lps, bl, sc_in, n_layers, L):
+    """Oracle (torch on the host) on a bounded sample of the same step, scaled to 30 layers."""
+    import torch.nn.functional as Fn
+    from oracle import llama as OL
+    from oracle import scoring as OS
+    from oracle.schedule import omnivoice_unmask_schedule, quantile_fractions
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    B = len(lps)
+    Bp = B // 2
+    bb = OL.backbone_from_model(model, max_pos=max(lps) + 2 * bl, dtype=torch.bfloat16)
+    cache = OL.KVCache(k=[], v=[])
+    g = torch.Generator().manual_seed(99)
+    for _ in range(n_layers):
+        cache.k.append([torch.randn(lp + bl, 16, 64, generator=g).bfloat16() for lp in lps])
+        cache.v.append([torch.randn(lp + bl, 16, 64, generator=g).bfloat16() for lp in lps])
+    block = torch.randn(B, bl, 1024, generator=g).bfloat16()
+    ctx = torch.randn(B, 1, 1024, generator=g).bfloat16()
+    OL.block_forward(bb, block[:2], OL.KVCache(k=[c[:2] for c in cache.k], v=[c[:2] for c in cache.v]),
+                     lps[:2], n_layers=1)  # warm-up
+    t = time.time()
+    hid = OL.block_forward(bb, block, cache, lps, n_layers=n_layers)
+    t_layers = time.time() - t
+    t = time.time()
+    logits = OL.speech_head_shift(hid, ctx, model.speech_head.weight.detach().cpu().bfloat16())
+    t_head = time.time() - t
+    t = time.time()
+    sched = torch.tensor(omnivoice_unmask_schedule(bl, 10, 0.5))
+    q = torch.tensor(quantile_fractions(3.0, 10), dtype=torch.float32)
+    OS.score_step(logits[:Bp].float(), logits[Bp:].float(), sc_in.xt.cpu(), sc_in.k_step.cpu(),
+                  sc_in.log_prior.cpu(), sched, q, K=10, cfg=0.5, tau=3.0, mask_id=8194, stop_id=6562)
+    t_score = time.time() - t
+    t_step = t_layers * L / n_layers + t_head + t_score
+    log(f"cpu baseline: {n_layers} layers {t_layers:.2f}s, head {t_head:.2f}s, score {t_score:.2f}s "
+        f"-> {t_step:.1f}s per step on {threads} threads")
+    return {"value": round(Bp * bl / t_step, 2), "unit": "speech tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle torch-CPU bf16 block forward of {n_layers} of {L} layers at the full "
+                      f"{B}-row batch (time x {L}/{n_layers}) + speech head + fp32 scoring; "
+                      f"{t_step:.1f} s per step"}
+
+
+if __name__ == "__main__":
+    main()
