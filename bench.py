@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-sample", action="store_true",
+                    help="only run the dominant GEMM (bench shape) and a 1 GiB copy, for rocprofv3 --pmc")
     return ap.parse_args()
 
 
@@ -83,6 +85,9 @@ def main():
     kernels.load_library()
     dev = torch.device("cuda:0")
     Bp, bl, L = args.pairs, args.block, args.layers
+    if args.kernel_sample:
+        kernel_sample(dev, 2 * Bp * bl)
+        return
     B = 2 * Bp
     D, H, F, V = 1024, 16, 4096, 8194
     t0 = time.time()
@@ -141,6 +146,11 @@ def main():
         step.scorer(sets[it[0]], step.xt, step.k_step, layout="stacked")
     ms_score = time_launches(score_once, 20, dev)
 
+    csrc = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    cdst = torch.empty_like(csrc)
+    ms_copy = time_launches(lambda: cdst.copy_(csrc), 10, dev)
+    copy_gbs = 2 * COPY_BYTES / (ms_copy * 1e-3) / 1e9
+    del csrc, cdst
     flops_swiglu = 2.0 * N * (2 * F) * D
     tf_swiglu = flops_swiglu / (ms_swiglu * 1e-3) / 1e12
     kv_len = plan.kv_len.tolist()
@@ -193,10 +203,33 @@ def main():
                         "unit": "GB/s", "frac": round(gbs_score / HBM_PEAK_GBS, 4)},
             "gemm_us": {"qkv_rope_kv": round(ms_qkv * 1e3, 1), "o_proj": round(ms_o * 1e3, 1),
                         "gate_up_swiglu": round(ms_swiglu * 1e3, 1), "down": round(ms_down * 1e3, 1)},
+            "measured_copy_GBps": round(copy_gbs, 1),
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+COPY_BYTES = 1 << 30
+
+
+def kernel_sample(dev, N):
+    """The dominant kernel at the bench shape plus a plain 1 GiB device copy (the
+    FETCH_SIZE / WRITE_SIZE calibration), three dispatches each."""
+    from yapd_amd import kernels
+    g = torch.Generator(device=dev).manual_seed(0)
+    A = torch.randn(N, 1024, generator=g, device=dev).bfloat16()
+    W = (torch.randn(8192, 1024, generator=g, device=dev) * 0.02).bfloat16()
+    act = torch.empty(N, 4096, dtype=torch.bfloat16, device=dev)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize(dev)
+    for _ in range(3):
+        kernels.gemm_swiglu(A, W, act)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    print(json.dumps({"kernel_sample": "gemm_swiglu M=%d N=8192 K=1024 x3; copy %d bytes x3" % (N, COPY_BYTES)}))
 
 
 def cpu_baseline(model, eng, lps, bl, sc_in, n_layers, L):

@@ -153,6 +153,16 @@ int yapd_gemm_head_shift(const void* hidden, const void* shift_ctx, int rows, in
 int yapd_rmsnorm(const void* delta, void* residual, const void* x, const void* w, float eps, int M, int D,
                  void* out, void* stream);
 
+/* (d) Affine group-quantised projection, MLX layout (engines/mlx.py:221-255
+ * quantises with mlx.nn.quantize): w_packed uint32 [N, K*bits/32] holds
+ * LSB-first codes, scales and biases fp16 [N, K/64]; W_hat = scale*q + bias
+ * per group of 64 input features, dequantised into the MFMA B tile.
+ * C[M, N] = A[M, K] W_hat^T in bf16 with fp32 accumulation; bits 4 or 8,
+ * group_size 64. */
+int yapd_qgemm_affine(const void* A, int64_t lda, const uint32_t* w_packed, const void* scales,
+                      const void* biases, int bits, int group_size, int M, int N, int K, void* C, int64_t ldc,
+                      void* stream);
+
 /* ------------------------------------------------------------------------ *
  * Whole block forward: one call runs the n_layers decoder layers and the
  * final norm (engines/flashinfer.py:_block_forward_fused :970-1065 /

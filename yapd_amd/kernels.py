@@ -46,6 +46,8 @@ _SIGNATURES = {
     "yapd_gemm_qkv_rope_kv": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_int, c_void,
                                       c_int, c_void, c_void, c_i64, c_void, c_int, c_int, c_void]),
     "yapd_rmsnorm": (c_int, [c_void, c_void, c_void, c_void, c_float, c_int, c_int, c_void, c_void]),
+    "yapd_qgemm_affine": (c_int, [c_void, c_i64, c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_int,
+                                  c_void, c_i64, c_void]),
     "yapd_t3_block_forward": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void, c_int, c_void,
                                       c_void, c_int, c_void, c_void, c_i64, c_void]),
 }
