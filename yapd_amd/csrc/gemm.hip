@@ -230,8 +230,10 @@ __device__ __forceinline__ uint32_t dq_pair(uint32_t word, int shift, float sc, 
 
 template <class T, int EPI, int AM, int BQ = 0>
 __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][T::BM * T::PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][T::BN * T::PITCH];
+  // One LDS block: two A stages, then two B stages; the store epilogue reuses all of it.
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (T::BM + T::BN) * T::PITCH];
+  uint16_t(*sA)[T::BM * T::PITCH] = reinterpret_cast<uint16_t(*)[T::BM * T::PITCH]>(smem);
+  uint16_t(*sB)[T::BN * T::PITCH] = reinterpret_cast<uint16_t(*)[T::BN * T::PITCH]>(smem + 2 * T::BM * T::PITCH);
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave / T::WN, wn = wave % T::WN;
@@ -351,35 +353,46 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
       bfr[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(b_l + 32 * j * T::PITCH));
   };
 
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+  };
+  // MFMAs of one k-step interleaved with the TM + TN fragment reads of the next.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int r = 0; r < T::TM + T::TN; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, (T::TM * T::TN) / (T::TM + T::TN), 0);  // MFMAs
+    }
+  };
+
+  // Pipeline: the last k-step of tile kt is multiplied after the barrier, so
+  // its MFMAs (register operands only) cover the first LDS reads of tile kt+1.
   fetch(0);
   stash(0);
   __syncthreads();
+  read_frags(0, 0, 0);
   for (int kt = 0; kt < kt_n; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < kt_n) fetch((kt + 1) * T::BK);
-    read_frags(buf, 0, 0);
+    const bool more = kt + 1 < kt_n;
+    if (more) fetch((kt + 1) * T::BK);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) read_frags(buf, ks + 1, (ks + 1) & 1);
-#pragma unroll
-      for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < T::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
-      // Interleave the next step's LDS reads with this step's MFMAs.
-      if (ks + 1 < KS) {
-#pragma unroll
-        for (int r = 0; r < T::TM + T::TN; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, (T::TM * T::TN) / (T::TM + T::TN), 0);  // MFMAs
-        }
-      }
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      read_frags(buf, ks + 1, (ks + 1) & 1);
+      mfma_step(ks & 1);
+      interleave();
     }
-    if (kt + 1 < kt_n) stash(buf ^ 1);
+    if (more) stash(buf ^ 1);
     __syncthreads();
+    if (more) read_frags(buf ^ 1, 0, 0);
+    mfma_step((KS - 1) & 1);
+    if (more) interleave();
   }
   if (EPI == kEpiStore) {
-    store_tile_via_lds<T>(p, acc, reinterpret_cast<uint16_t*>(sA), m0, n0, wm, wn, lane, tid);
+    store_tile_via_lds<T>(p, acc, smem, m0, n0, wm, wn, lane, tid);
   } else {
     epilogue<EPI, T::TM, T::TN>(p, acc, m0 + wm * T::WTM, n0 + wn * T::WTN, lane);
   }
