@@ -129,8 +129,10 @@ int yapd_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, int M
 
 /* Fused QKV + NeoX RoPE + paged KV write (engines/flashinfer.py:998-1035):
  * rows r*bl+j at position pos0[r]+j; cos/sin fp32 [max_pos, 64] hold the
- * model-dtype table (flashinfer.py:246-255); q goes to q_out [M, H*64], k
- * and v straight into the pool. */
+ * model-dtype table (flashinfer.py:246-255) in HF's cat(freqs, freqs)
+ * layout: column d + 32 must equal column d, and only columns 0..31 are
+ * read.  q goes to q_out [M, H*64], k and v straight into the pool
+ * (n_pages < 2^31). */
 int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
                           const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int bl,
                           void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride,

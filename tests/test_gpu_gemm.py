@@ -23,8 +23,10 @@ def rel_err(out, ref):
     return ((out.float() - ref.float()).abs().max() / ref.float().abs().max().clamp_min(1e-6)).item()
 
 
+# The last three take the large-tile (256 x 256) path: >= 256 output tiles,
+# M not a multiple of 256 in two of them.
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 3072, 1024), (1024, 1024, 4096), (37, 8194, 1024),
-                                   (16384 // 8, 8192, 1024)])
+                                   (16384 // 8, 8192, 1024), (2000, 8192, 1024), (4100, 4096, 2048)])
 def test_gemm_bf16(dev, M, N, K):
     A = rnd(M, K, seed=1)
     W = rnd(N, K, std=0.02, seed=2)
@@ -47,8 +49,9 @@ def test_gemm_padded_ldc_and_strided_a(dev):
     assert torch.count_nonzero(out_full[:, N:]) == 0  # nothing written past N
 
 
-def test_gemm_swiglu(dev):
-    M, K, Fd = 300, 1024, 4096
+@pytest.mark.parametrize("M", [300, 2000])  # 2000: large-tile path
+def test_gemm_swiglu(dev, M):
+    K, Fd = 1024, 4096
     A = rnd(M, K, seed=5)
     Wg = rnd(Fd, K, std=0.02, seed=6)
     Wu = rnd(Fd, K, std=0.02, seed=7)
@@ -60,8 +63,9 @@ def test_gemm_swiglu(dev):
     assert rel_err(act.cpu(), ref.float()) <= 1.5e-2
 
 
-def test_gemm_head_shift(dev):
-    rows, bl, D, V = 6, 32, 1024, 8194
+@pytest.mark.parametrize("rows", [6, 70])  # 70 x 32 rows: large-tile path
+def test_gemm_head_shift(dev, rows):
+    bl, D, V = 32, 1024, 8194
     hidden = rnd(rows, bl, D, seed=8)
     ctx = rnd(rows, 1, D, seed=9)
     W = rnd(V, D, std=0.02, seed=10)
@@ -71,21 +75,20 @@ def test_gemm_head_shift(dev):
     assert rel_err(logits.cpu(), ref) <= 8e-3
 
 
-def test_gemm_qkv_rope_kv(dev):
-    from types import SimpleNamespace
-    from tests.test_oracle_llama import tiny_model  # noqa: F401 (rotary table helper below)
-    H, D, rows, bl = 16, 1024, 3, 32
+@pytest.mark.parametrize("rows", [3, 180])  # 180 x 32 rows: large-tile path
+def test_gemm_qkv_rope_kv(dev, rows):
+    H, D, bl = 16, 1024, 32
     M = rows * bl
     A = rnd(M, D, seed=11)
     Wqkv = rnd(3 * H * 64, D, std=0.02, seed=12)
-    pos0 = [7, 150, 600]
+    pos0 = [7, 150, 600] if rows == 3 else np.random.default_rng(1).integers(0, 700, rows).tolist()
     # HF default RoPE table (theta 10000) in the model dtype, as the engine builds it
     inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
     t = torch.arange(1024).float()
     fr = torch.outer(t, inv)
     emb = torch.cat([fr, fr], -1)
     cos_b, sin_b = emb.cos().bfloat16(), emb.sin().bfloat16()
-    n_pages = 160
+    n_pages = rows * 48 + 16
     table = np.random.default_rng(0).permutation(n_pages)[: rows * 48].reshape(rows, 48).astype(np.int32)
     pool = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
     q_out = torch.empty(M, H * 64, dtype=torch.bfloat16, device=dev)

@@ -60,7 +60,7 @@ struct GemmParams {
   uint16_t* C;
   int64_t ldc;
   // qkv epilogue
-  const float* cos_t;  // [max_pos, 64] fp32 (values of the model-dtype table)
+  const float* cos_t;  // [max_pos, 64] fp32 (values of the model-dtype table; columns 0..31 are read)
   const float* sin_t;
   int max_pos;
   const int32_t* pos0;  // [M / bl] first position of each row's block
@@ -93,88 +93,159 @@ __device__ __forceinline__ const uint16_t* a_row_ptr(const GemmParams& p, int m)
 
 __device__ __forceinline__ float bf16r(float x) { return round_bf16(x); }
 
-template <int EPI, int TM, int TN>
-__device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16_t (&acc)[TM][TN], int m_base, int n_base,
-                                         int lane) {
-  const int col = lane & 31;
-  const int rgrp = 4 * (lane >> 5);
-  if (EPI == kEpiStore) {
+// Position and KV page of one tile row for the qkv epilogue.  Computed at
+// kernel start by thread `row` (< BM), so the loads of pos0 and of the page
+// table overlap the main loop; parked in LDS for the epilogue.
+struct RowMeta {
+  int pos, page;
+};
+
+template <class T>
+__device__ __forceinline__ RowMeta qkv_row_meta(const GemmParams& p, int m0, int row) {
+  RowMeta rm{0, 0};
+  if (row < T::BM) {
+    const int m = min(m0 + row, p.M - 1);
+    const int r = m / p.bl;
+    const int pos = p.pos0[r] + (m - r * p.bl);
+    const int pi = min(max(pos, 0) / kPageSize, p.table_cols - 1);
+    int64_t page = p.table[static_cast<int64_t>(r) * p.table_stride + pi];
+    page = min(max(page, int64_t{0}), p.n_pages - 1);
+    rm.pos = pos;
+    rm.page = static_cast<int>(page);
+  }
+  return rm;
+}
+
+// qkv epilogue: tiles 2q, 2q+1 of a wave are head dims d and d + 32 of one
+// head of q, k or v (n_base is a multiple of 64 and 64 divides n_heads * 64).
+// NeoX RoPE on q and k from the cos/sin tables at each row's position; the
+// tables are HF's cat(freqs, freqs) layout, so column d + 32 equals column d
+// and only columns 0..31 are read.  `lds` holds the RowMeta of the tile rows.
+// qkv epilogue.  The qkv GEMM multiplies W x A^T (MFMA operands swapped), so
+// lane l holds token (l & 31) of each 32-row block and, in each 32-column
+// block, head dims 8 * (e / 4) + 4 * (l / 32) + e % 4 for accumulator
+// element e: four runs of 4 consecutive dims.  Tiles 2q, 2q+1 of a wave are
+// dims d and d + 32 of one head of q, k or v (the section is uniform per
+// wave: n_base is a multiple of 64 and 64 divides n_heads * 64).  So a lane
+// does RoPE on whole runs (16-byte cos/sin loads), stores q and k as 8-byte
+// runs, and a V column (layout d * 16 + slot) is written by 32 lanes with
+// consecutive slots.  `meta` holds the RowMeta of the tile rows.
+template <class T, int SECTION>
+__device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
+                                                     const RowMeta* meta, int m0, int nb, int q2, int wm, int lane) {
+  const int tok = lane & 31;
+  const int dgrp = 4 * (lane >> 5);
+  const int HD = p.n_heads * kHeadDim;
+  const int head = (nb - SECTION * HD) / kHeadDim;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < T::TM; ++i) {
+    const int rl = wm * T::WTM + 32 * i + tok;
+    const int m = m0 + rl;
+    if (m >= p.M) continue;
+    const RowMeta mt = meta[rl];
+    const int pc = min(max(mt.pos, 0), p.max_pos - 1);
+    const int slot = mt.pos & (kPageSize - 1);
+    uint16_t* const kv = p.pool + kv_plane_offset(mt.page, SECTION == 2 ? 1 : 0, head, p.n_heads);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n_base + 32 * j + col;
-        if (n >= p.N) continue;
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d0 = 8 * r4 + dgrp;
+      float x0[4], x1[4];  // dims d0 + t and d0 + 32 + t
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m_base + 32 * i + 8 * (e >> 2) + rgrp + (e & 3);
-          if (m < p.M) p.C[static_cast<int64_t>(m) * p.ldc + n] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][e]));
+      for (int t = 0; t < 4; ++t) {
+        x0[t] = bf16r(acc[i][2 * q2][4 * r4 + t]);
+        x1[t] = bf16r(acc[i][2 * q2 + 1][4 * r4 + t]);
+      }
+      if constexpr (SECTION < 2) {
+        const f32x4_t c = *reinterpret_cast<const f32x4_t*>(p.cos_t + pc * kHeadDim + d0);
+        const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(p.sin_t + pc * kHeadDim + d0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          // x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1], each op rounded to bf16
+          const float y0 = bf16r(bf16r(x0[t] * c[t]) + bf16r(-x1[t] * sn[t]));
+          const float y1 = bf16r(bf16r(x1[t] * c[t]) + bf16r(x0[t] * sn[t]));
+          x0[t] = y0;
+          x1[t] = y1;
         }
       }
-  } else if (EPI == kEpiSwiglu) {
-    // Each 64-column group of W holds gate rows of 32 features, then their up rows:
-    // tile 2q is gate and tile 2q+1 is up of features f = (n_base + 64q)/2 + col.
+      const u32x2_t lo = {pack_bf16x2(x0[0], x0[1]), pack_bf16x2(x0[2], x0[3])};
+      const u32x2_t hi = {pack_bf16x2(x1[0], x1[1]), pack_bf16x2(x1[2], x1[3])};
+      if constexpr (SECTION == 0) {
+        uint16_t* qp = p.q_out + static_cast<int64_t>(m) * HD + head * kHeadDim + d0;
+        *reinterpret_cast<u32x2_t*>(qp) = lo;
+        *reinterpret_cast<u32x2_t*>(qp + 32) = hi;
+      } else if constexpr (SECTION == 1) {
+        *reinterpret_cast<u32x2_t*>(kv + slot * kHeadDim + d0) = lo;
+        *reinterpret_cast<u32x2_t*>(kv + slot * kHeadDim + d0 + 32) = hi;
+      } else {
 #pragma unroll
-    for (int q2 = 0; q2 < TN / 2; ++q2) {
-      const int f = ((n_base + 64 * q2) >> 1) + col;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m_base + 32 * i + 8 * (e >> 2) + rgrp + (e & 3);
-          if (m >= p.M) continue;
-          const float g = bf16r(acc[i][2 * q2][e]);
-          const float u = bf16r(acc[i][2 * q2 + 1][e]);
-          const float s = bf16r(g / (1.f + __expf(-g)));
-          p.C[static_cast<int64_t>(m) * p.ldc + f] = static_cast<uint16_t>(f32_to_bf16(s * u));
+        for (int t = 0; t < 4; ++t) {
+          kv[(d0 + t) * kPageSize + slot] = static_cast<uint16_t>(f32_to_bf16(x0[t]));
+          kv[(d0 + 32 + t) * kPageSize + slot] = static_cast<uint16_t>(f32_to_bf16(x1[t]));
         }
+      }
     }
-  } else {  // kEpiQkv: tiles 2q, 2q+1 are head dims d and d + 32 of one head of q, k or v
-    const int HD = p.n_heads * kHeadDim;
-    const int d = col;
+  }
+}
+
+template <class T>
+__device__ __forceinline__ void epilogue_qkv(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
+                                             const RowMeta* meta, int m0, int n_base, int wm, int lane) {
+  const int HD = p.n_heads * kHeadDim;
 #pragma unroll
-    for (int q2 = 0; q2 < TN / 2; ++q2) {
-      const int nb = n_base + 64 * q2;
-      const int section = nb / HD;  // 0 q, 1 k, 2 v
-      const int head = (nb - section * HD) / kHeadDim;
+  for (int q2 = 0; q2 < T::TN / 2; ++q2) {
+    const int nb = n_base + 64 * q2;
+    const int section = nb / HD;  // 0 q, 1 k, 2 v
+    if (section == 0) {
+      epilogue_qkv_section<T, 0>(p, acc, meta, m0, nb, q2, wm, lane);
+    } else if (section == 1) {
+      epilogue_qkv_section<T, 1>(p, acc, meta, m0, nb, q2, wm, lane);
+    } else {
+      epilogue_qkv_section<T, 2>(p, acc, meta, m0, nb, q2, wm, lane);
+    }
+  }
+}
+
+// swiglu epilogue: each 64-column group of W holds the gate rows of 32
+// features, then their up rows, so tile 2q is gate and tile 2q+1 is up of
+// features (n_base + 64q)/2 + col.  silu(g) and the product are rounded to
+// bf16 as the reference's separate ops are; silu uses the hardware
+// reciprocal (<= 1 ulp in fp32 before the bf16 rounding).  The bf16 results
+// are parked in LDS and written as 16-byte row chunks.
+template <class T>
+__device__ __forceinline__ void epilogue_swiglu(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
+                                                uint16_t* lds, int m0, int n0, int wm, int wn, int lane, int tid) {
+  constexpr int FW = T::BN / 2;  // features per workgroup tile
+  constexpr int CP = FW + 8;     // staging row pitch (bf16)
+  const int col = lane & 31;
+  const int rgrp = 4 * (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+  for (int q2 = 0; q2 < T::TN / 2; ++q2) {
+    const int fl = wn * (T::WTN / 2) + 32 * q2 + col;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m_base + 32 * i + 8 * (e >> 2) + rgrp + (e & 3);
-          if (m >= p.M) continue;
-          const int r = m / p.bl;
-          const int pos = p.pos0[r] + (m - r * p.bl);
-          float x0 = bf16r(acc[i][2 * q2][e]);      // element d
-          float x1 = bf16r(acc[i][2 * q2 + 1][e]);  // element d + 32
-          if (section < 2) {
-            const int pc = min(max(pos, 0), p.max_pos - 1);
-            const float c0 = p.cos_t[pc * kHeadDim + d], c1 = p.cos_t[pc * kHeadDim + d + 32];
-            const float s0 = p.sin_t[pc * kHeadDim + d], s1 = p.sin_t[pc * kHeadDim + d + 32];
-            // x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1], each op rounded to bf16
-            const float y0 = bf16r(bf16r(x0 * c0) + bf16r(-x1 * s0));
-            const float y1 = bf16r(bf16r(x1 * c1) + bf16r(x0 * s1));
-            x0 = y0;
-            x1 = y1;
-          }
-          if (section == 0) {
-            uint16_t* qp = p.q_out + static_cast<int64_t>(m) * HD + head * kHeadDim;
-            qp[d] = static_cast<uint16_t>(f32_to_bf16(x0));
-            qp[d + 32] = static_cast<uint16_t>(f32_to_bf16(x1));
-          } else {
-            const int pi = min(max(pos, 0) / kPageSize, p.table_cols - 1);
-            int64_t page = p.table[static_cast<int64_t>(r) * p.table_stride + pi];
-            page = min(max(page, int64_t{0}), p.n_pages - 1);
-            const int slot = pos & (kPageSize - 1);
-            if (section == 1) {
-              p.pool[k_offset(page, head, p.n_heads, slot, d)] = static_cast<uint16_t>(f32_to_bf16(x0));
-              p.pool[k_offset(page, head, p.n_heads, slot, d + 32)] = static_cast<uint16_t>(f32_to_bf16(x1));
-            } else {
-              p.pool[v_offset(page, head, p.n_heads, slot, d)] = static_cast<uint16_t>(f32_to_bf16(x0));
-              p.pool[v_offset(page, head, p.n_heads, slot, d + 32)] = static_cast<uint16_t>(f32_to_bf16(x1));
-            }
-          }
-        }
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rl = wm * T::WTM + 32 * i + 8 * (e >> 2) + rgrp + (e & 3);
+        const float g = bf16r(acc[i][2 * q2][e]);
+        const float u = bf16r(acc[i][2 * q2 + 1][e]);
+        const float s = bf16r(g * __builtin_amdgcn_rcpf(1.f + __expf(-g)));
+        lds[rl * CP + fl] = static_cast<uint16_t>(f32_to_bf16(s * u));
+      }
+  }
+  __syncthreads();
+  const int F = p.N / 2, f0 = n0 / 2;
+  const bool vec_ok = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
+  constexpr int CPR = FW / 8;
+  for (int idx = tid; idx < T::BM * CPR; idx += T::THREADS) {
+    const int r = idx / CPR, cc = (idx % CPR) * 8;
+    const int m = m0 + r, f = f0 + cc;
+    if (m >= p.M || f >= F) continue;  // F % 64 == 0: a chunk is all in or all out
+    const uint16_t* src = lds + r * CP + cc;
+    uint16_t* dst = p.C + static_cast<int64_t>(m) * p.ldc + f;
+    if (vec_ok) {
+      *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
+    } else {
+      for (int t = 0; t < 8; ++t) dst[t] = src[t];
     }
   }
 }
@@ -228,6 +299,24 @@ __device__ __forceinline__ uint32_t dq_pair(uint32_t word, int shift, float sc, 
   return pack_bf16x2(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
 }
 
+// Epilogue dispatch.  Every wave has finished reading the LDS stages (the
+// main loop ends with a barrier and no LDS reads after it), so the epilogues
+// may reuse all of LDS.
+template <class T, int EPI>
+__device__ __forceinline__ void finish_tile(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN], uint16_t* lds,
+                                            const RowMeta& rm, int m0, int n0, int wm, int wn, int lane, int tid) {
+  if constexpr (EPI == kEpiStore) {
+    store_tile_via_lds<T>(p, acc, lds, m0, n0, wm, wn, lane, tid);
+  } else if constexpr (EPI == kEpiSwiglu) {
+    epilogue_swiglu<T>(p, acc, lds, m0, n0, wm, wn, lane, tid);
+  } else {
+    RowMeta* meta = reinterpret_cast<RowMeta*>(lds);
+    if (tid < T::BM) meta[tid] = rm;
+    __syncthreads();
+    epilogue_qkv<T>(p, acc, meta, m0, n0 + wn * T::WTN, wm, lane);
+  }
+}
+
 template <class T, int EPI, int AM, int BQ = 0>
 __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
   // One LDS block: two A stages, then two B stages; the store epilogue reuses all of it.
@@ -235,7 +324,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
   uint16_t(*sA)[T::BM * T::PITCH] = reinterpret_cast<uint16_t(*)[T::BM * T::PITCH]>(smem);
   uint16_t(*sB)[T::BN * T::PITCH] = reinterpret_cast<uint16_t(*)[T::BN * T::PITCH]>(smem + 2 * T::BM * T::PITCH);
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // wave index: uniform
   const int wm = wave / T::WN, wn = wave % T::WN;
   const int m0 = blockIdx.y * T::BM, n0 = blockIdx.x * T::BN;
 
@@ -358,7 +447,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
       for (int j = 0; j < T::TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = EPI == kEpiQkv  // transposed product for the qkv epilogue
+                        ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0)
+                        : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
   };
   // MFMAs of one k-step interleaved with the TM + TN fragment reads of the next.
   auto interleave = [&]() {
@@ -372,6 +463,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
   // Pipeline: the last k-step of tile kt is multiplied after the barrier, so
   // its MFMAs (register operands only) cover the first LDS reads of tile kt+1.
   fetch(0);
+  const RowMeta rm = EPI == kEpiQkv ? qkv_row_meta<T>(p, m0, tid) : RowMeta{0, 0};
   stash(0);
   __syncthreads();
   read_frags(0, 0, 0);
@@ -391,11 +483,159 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
     mfma_step((KS - 1) & 1);
     if (more) interleave();
   }
-  if (EPI == kEpiStore) {
-    store_tile_via_lds<T>(p, acc, smem, m0, n0, wm, wn, lane, tid);
-  } else {
-    epilogue<EPI, T::TM, T::TN>(p, acc, m0 + wm * T::WTM, n0 + wn * T::WTN, lane);
+  finish_tile<T, EPI>(p, acc, smem, rm, m0, n0, wm, wn, lane, tid);
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant for bf16 W.  A and W tiles travel global -> LDS with
+// global_load_lds_dwordx4 (64 lanes x 16 bytes land as one contiguous 1 KB
+// run at the wave-uniform LDS address in M0), so there is no register
+// staging and no ds_write: LDS writes through ds_write_b128 sustain about a
+// third of the ds_read_b128 rate on gfx950 and were the bound of the staged
+// kernel.
+//
+// LDS rows hold BK = 64 bf16 (128 bytes) unpadded.  The 16-byte chunk c of
+// row r sits in slot c ^ ((r >> 1) & 7): the 16 consecutive rows one
+// 16-lane group of a fragment read touches then cover 16 distinct 16-byte
+// bank groups (two 128-byte rows share one 256-byte bank line).  A load
+// instruction covers 8 rows; lane i writes slot i % 8 of row i / 8, so it
+// fetches the chunk that belongs there.
+template <class T>
+struct DlLayout {
+  static_assert(T::BK == 64, "direct-load tiles use 128-byte LDS rows");
+  static constexpr int WAVES = T::THREADS / 64;
+  static constexpr int ROWB = 128;
+  static constexpr int A_BYTES = T::BM * ROWB, B_BYTES = T::BN * ROWB;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int LA = T::BM / 8 / WAVES;  // 1 KB loads per wave and k-tile
+  static constexpr int LB = T::BN / 8 / WAVES;
+  static_assert(LA * 8 * WAVES == T::BM && LB * 8 * WAVES == T::BN, "rows must split evenly over the waves");
+  static constexpr int C_BYTES = T::BM * (T::BN + 8) * 2;  // store-epilogue staging
+  static constexpr int LDS = 2 * STAGE > C_BYTES ? 2 * STAGE : C_BYTES;
+};
+
+// 16 bytes per lane from src into LDS at lds_run + 16 * lane (lds_run must be
+// the same for the whole wave: it is the M0 base of global_load_lds_dwordx4).
+__device__ __forceinline__ void load_lds16(const uint16_t* src, char* lds_run) {
+  __builtin_amdgcn_global_load_lds(
+      src, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(lds_run)), 16, 0, 0);
+}
+
+template <class T, int EPI, int AM>
+__global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p) {
+  using L = DlLayout<T>;
+  // Dynamic LDS: the compiler cannot see the DMA writes into a static
+  // __shared__ array and would treat its contents as undefined.
+  extern __shared__ __attribute__((aligned(16))) uint16_t dyn_lds[];
+  char* lds = reinterpret_cast<char*>(dyn_lds);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // wave index: uniform
+  const int wm = wave / T::WN, wn = wave % T::WN;
+  const int m0 = blockIdx.y * T::BM, n0 = blockIdx.x * T::BN;
+
+  // Per-lane sources of this wave's LA + LB loads (k offset added per tile).
+  // Rows past M (N) re-read the last valid row, as in the staged kernel.
+  const uint16_t* a_src[L::LA];
+  const uint16_t* b_src[L::LB];
+#pragma unroll
+  for (int j = 0; j < L::LA; ++j) {
+    const int r = (wave * L::LA + j) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_src[j] = a_row_ptr<AM>(p, min(m0 + r, p.M - 1)) + 8 * c;
   }
+#pragma unroll
+  for (int j = 0; j < L::LB; ++j) {
+    const int r = (wave * L::LB + j) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    b_src[j] = p.W + static_cast<int64_t>(min(n0 + r, p.N - 1)) * p.ldw + 8 * c;
+  }
+  auto issue = [&](int kt, int stage) {
+    const int k = kt * T::BK;
+    char* a_dst = lds + stage * L::STAGE + wave * L::LA * 1024;
+    char* b_dst = lds + stage * L::STAGE + L::A_BYTES + wave * L::LB * 1024;
+#pragma unroll
+    for (int j = 0; j < L::LA; ++j) load_lds16(a_src[j] + k, a_dst + j * 1024);
+#pragma unroll
+    for (int j = 0; j < L::LB; ++j) load_lds16(b_src[j] + k, b_dst + j * 1024);
+  };
+
+  f32x16_t acc[T::TM][T::TN];
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment addressing: lane l reads row (l & 31) of a 32-row MFMA tile,
+  // logical chunk 2 * ks + (l >> 5); the swizzle term depends on the lane
+  // only because every tile starts at a multiple of 16 rows.
+  const int frag_row = lane & 31;
+  const int ysw = (lane >> 5) ^ ((frag_row >> 1) & 7);
+  const int a_off = (wm * T::WTM + frag_row) * L::ROWB;
+  const int b_off = L::A_BYTES + (wn * T::WTN + frag_row) * L::ROWB;
+  constexpr int KS = T::BK / 16;
+  bf16x8_t af[2][T::TM], bfr[2][T::TN];
+  auto read_frags = [&](int stage, int ks, int slot) {
+    const int cofs = ((2 * ks) ^ ysw) * 16;
+    const char* a_l = lds + stage * L::STAGE + a_off + cofs;
+    const char* b_l = lds + stage * L::STAGE + b_off + cofs;
+    // Issue order = first use by mfma_step (i-major): A0, B0..B(TN-1), A1, ...
+    // LDS reads complete in order, so the wait before each MFMA only covers
+    // the reads it needs.
+    af[slot][0] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(a_l));
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+      bfr[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(b_l + 32 * j * L::ROWB));
+#pragma unroll
+    for (int i = 1; i < T::TM; ++i)
+      af[slot][i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(a_l + 32 * i * L::ROWB));
+  };
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+        acc[i][j] = EPI == kEpiQkv  // transposed product for the qkv epilogue
+                        ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0)
+                        : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+  };
+  // One MFMA, then one fragment read of the next k-step: the step's first
+  // MFMAs never wait on a read issued in the same step.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int r = 0; r < T::TM + T::TN; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, T::TM * T::TN - (T::TM + T::TN), 0);
+  };
+
+  // Two LDS stages.  Tile kt+1 is requested at the top of tile kt (its stage
+  // was last read in tile kt-1, before the barrier that ended it); the
+  // barrier at the end of tile kt waits for this wave's loads (the fence of
+  // __syncthreads drains vmcnt) and for every wave's.
+  const int kt_n = p.K / T::BK;
+  issue(0, 0);
+  const RowMeta rm = EPI == kEpiQkv ? qkv_row_meta<T>(p, m0, tid) : RowMeta{0, 0};
+  __syncthreads();
+  read_frags(0, 0, 0);
+  for (int kt = 0; kt < kt_n; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < kt_n;
+    if (more) issue(kt + 1, buf ^ 1);
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      read_frags(buf, ks + 1, (ks + 1) & 1);
+      mfma_step(ks & 1);
+      interleave();
+    }
+    __syncthreads();
+    if (more) read_frags(buf ^ 1, 0, 0);
+    mfma_step((KS - 1) & 1);
+    if (more) interleave();
+  }
+  finish_tile<T, EPI>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -476,11 +716,33 @@ int launch_tile(const GemmParams& p, hipStream_t st) {
   return YAPD_OK;
 }
 
+template <class T, int EPI, int AM>
+int launch_dl(const GemmParams& p, hipStream_t st) {
+  using L = DlLayout<T>;
+  static bool lds_set = false;  // the attribute is per kernel; setting it twice is harmless
+  if (!lds_set) {
+    if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dl_kernel<T, EPI, AM>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS),
+                           "gemm_dl_kernel LDS attribute"))
+      return rc;
+    lds_set = true;
+  }
+  const dim3 grid((p.N + T::BN - 1) / T::BN, (p.M + T::BM - 1) / T::BM), block(T::THREADS);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, EPI, AM>), grid, block, L::LDS, st, p);
+  YAPD_LAUNCH_CHECK("gemm_dl_kernel launch");
+  return YAPD_OK;
+}
+
+using TileD = Tile<256, 256, BK, 2, 4>;  // direct-load large tile
+
 template <int EPI, int AM, int BQ = 0>
 int launch_gemm(const GemmParams& p, hipStream_t st) {
   // Large tiles once they still give at least one workgroup per CU.
   const int64_t big_tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
-  if (big_tiles >= 256) return launch_tile<TileL, EPI, AM, BQ>(p, st);
+  if (big_tiles >= 256) {
+    if constexpr (BQ == 0) return launch_dl<TileD, EPI, AM>(p, st);
+    return launch_tile<TileL, EPI, AM, BQ>(p, st);
+  }
   return launch_tile<TileS, EPI, AM, BQ>(p, st);
 }
 
@@ -579,8 +841,11 @@ extern "C" int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_q
   p.table_cols = table_cols;
   if (int rc = yapd::check_common(p)) return rc;
   YAPD_REQUIRE(cos_t && sin_t && pos0 && q_out && kv_pool && page_table, "gemm_qkv: NULL pointer");
-  YAPD_REQUIRE(max_pos >= 1 && bl >= 1 && M % bl == 0 && n_heads >= 1 && n_pages >= 1 && table_cols >= 1 &&
-                   table_stride >= table_cols,
+  YAPD_REQUIRE(yapd::al16(cos_t) && yapd::al16(sin_t) && (reinterpret_cast<uintptr_t>(q_out) & 7u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(kv_pool) & 7u) == 0,
+               "gemm_qkv: cos/sin must be 16-byte aligned, q_out and kv_pool 8-byte aligned");
+  YAPD_REQUIRE(max_pos >= 1 && bl >= 1 && M % bl == 0 && n_heads >= 1 && n_pages >= 1 && n_pages <= INT32_MAX &&
+                   table_cols >= 1 && table_stride >= table_cols,
                "gemm_qkv: bad positions / table shape");
   return yapd::launch_gemm<yapd::kEpiQkv, yapd::kAPlain>(p, static_cast<hipStream_t>(stream));
 }

@@ -111,6 +111,11 @@ class HipEngine:
             cos, sin = tf.rotary_emb(dummy, torch.arange(self._max_seq_len, device=dev).unsqueeze(0))
             self._cos = cos[0].float().contiguous()
             self._sin = sin[0].float().contiguous()
+            # The fused qkv kernel reads columns 0..31 only: HF builds the tables
+            # as cat(freqs, freqs), so columns d and d + 32 are equal.
+            if not (torch.equal(self._cos[:, :32], self._cos[:, 32:])
+                    and torch.equal(self._sin[:, :32], self._sin[:, 32:])):
+                raise ValueError("rotary table is not in cat(freqs, freqs) layout; the hip qkv kernel needs it")
 
         # ---- paged KV ----
         self._pages_per_row = math.ceil(self._max_seq_len / PAGE_SIZE)

@@ -348,7 +348,10 @@ def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor
 def gemm_qkv_rope_kv(A: torch.Tensor, W_qkv: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor,
                      pos0: torch.Tensor, bl: int, q_out: torch.Tensor, pool: torch.Tensor,
                      table: torch.Tensor) -> None:
-    """Fused QKV projection + NeoX RoPE + paged KV write (q to ``q_out [M, H*64]``)."""
+    """Fused QKV projection + NeoX RoPE + paged KV write (q to ``q_out [M, H*64]``).
+
+    ``cos_t``/``sin_t`` are HF's [P, 64] tables (cat(freqs, freqs): column
+    d + 32 equals column d); the kernel reads columns 0..31."""
     dev = A.device
     _mat(A, "A", dev)
     require_cuda(W_qkv, "W_qkv", torch.bfloat16, dev)
