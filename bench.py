@@ -11,11 +11,19 @@ theta 10000, linear weights N(0, 0.02)), speech head V = 8194, then CFG
 scoring, replayed as one HIP graph.
 
 Prints one JSON line.  ``value`` = speech tokens/s = pairs * block / step time.
-``roofline`` describes the dominant kernel (the gate/up + SiLU GEMM);
-``kernels`` adds attention and scoring against the HBM roofline.  Per-kernel
-durations come from HIP events around single launches on the stream the
-kernel runs on, right after the timed region.  ``cpu_baseline`` times the
-oracle (torch on the host cores) on a bounded sample of the same step.
+``roofline`` describes the dominant kernel (the gate/up + SiLU GEMM) against
+the published bf16 peak and, as ``peak_measured``, against the sustained MFMA
+rate of a register-only calibration kernel; ``kernels`` adds attention and
+scoring against the HBM roofline.  Per-kernel durations come from HIP events
+around single launches on the stream the kernel runs on, right after the
+timed region.  ``cpu_baseline`` times the oracle (torch on the host cores) on
+a bounded sample of the same step.
+
+``--workload attn_stress`` instead measures 30 layers of block attention
+back to back over 256 sequences with log-uniform [64, 2048] prefixes, block
+16, each layer's pages drawn at random from its own 65,536-page pool; and
+``--workload quant`` the four 4-bit and 8-bit affine-quantised projections of
+30 layers at M = 8192.  Each prints its own JSON line.
 """
 
 from __future__ import annotations
@@ -47,6 +55,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["step", "attn_stress", "quant"], default="step")
     ap.add_argument("--kernel-sample", action="store_true",
                     help="only run the dominant GEMM (bench shape) and a 1 GiB copy, for rocprofv3 --pmc")
     return ap.parse_args()
@@ -88,6 +97,12 @@ def main():
     if args.kernel_sample:
         kernel_sample(dev, 2 * Bp * bl)
         return
+    if args.workload == "attn_stress":
+        attn_stress(args, dev)
+        return
+    if args.workload == "quant":
+        quant_projections(args, dev)
+        return
     B = 2 * Bp
     D, H, F, V = 1024, 16, 4096, 8194
     t0 = time.time()
@@ -122,17 +137,24 @@ def main():
     log(f"step {ms:.3f} ms")
 
     # ---- per-kernel durations (HIP events around single launches, same stream) ----
+    # Each launch takes the next layer's weights / KV pool, as the step does, so
+    # no launch finds its operands in the 256 MB MALL from the previous one.
     buf = eng._buffers(B, bl)
     plan = eng._g_plan
     N = B * bl
-    w0 = eng._w[0]
-    ms_swiglu = time_launches(lambda: kernels.gemm_swiglu(buf.normed, w0["wgu"], buf.act), 20, dev)
-    ms_qkv = time_launches(lambda: kernels.gemm_qkv_rope_kv(buf.normed, w0["wqkv"], eng._cos, eng._sin, buf.pos0,
-                                                            bl, buf.q, eng.kv.pools[0], eng.kv.table), 20, dev)
-    ms_o = time_launches(lambda: kernels.gemm_bf16(buf.attn, w0["wo"], buf.delta), 20, dev)
-    ms_down = time_launches(lambda: kernels.gemm_bf16(buf.act, w0["wd"], buf.delta), 20, dev)
+    layer = [0]
+
+    def nxt():
+        layer[0] = (layer[0] + 1) % L
+        return layer[0]
+    ms_swiglu = time_launches(lambda: kernels.gemm_swiglu(buf.normed, eng._w[nxt()]["wgu"], buf.act), 20, dev)
+    ms_qkv = time_launches(lambda: kernels.gemm_qkv_rope_kv(buf.normed, eng._w[nxt()]["wqkv"], eng._cos, eng._sin,
+                                                            buf.pos0, bl, buf.q, eng.kv.pools[layer[0]],
+                                                            eng.kv.table), 20, dev)
+    ms_o = time_launches(lambda: kernels.gemm_bf16(buf.attn, eng._w[nxt()]["wo"], buf.delta), 20, dev)
+    ms_down = time_launches(lambda: kernels.gemm_bf16(buf.act, eng._w[nxt()]["wd"], buf.delta), 20, dev)
     eager_plan = AttnPlan(plan.kv_len.tolist(), bl, H, dev)
-    ms_attn = time_launches(lambda: eager_plan.run(buf.q.view(B, bl, H, 64), eng.kv.pools[0], eng.kv.table,
+    ms_attn = time_launches(lambda: eager_plan.run(buf.q.view(B, bl, H, 64), eng.kv.pools[nxt()], eng.kv.table,
                                                    buf.attn.view(B, bl, H, 64), 0.125), 20, dev)
     # scoring on two rotated logits sets (the 268 MB input must not sit in the 256 MB MALL)
     sets = [eng._g_logits]
@@ -146,6 +168,7 @@ def main():
         step.scorer(sets[it[0]], step.xt, step.k_step, layout="stacked")
     ms_score = time_launches(score_once, 20, dev)
 
+    peak_meas = measured_mfma_peak(dev)
     csrc = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
     cdst = torch.empty_like(csrc)
     ms_copy = time_launches(lambda: cdst.copy_(csrc), 10, dev)
@@ -192,10 +215,13 @@ def main():
                    "hidden": D, "heads": H, "ffn": F, "vocab": V, "prefix_len": "U[150,600] per pair",
                    "page_table": "shuffled", "cfg_w": 0.5, "quantile_tau": 3.0, "K": 10},
         "rows_positions_per_s": round(B * bl / (ms * 1e-3), 1),
+        # one block costs K = 10 denoise steps + 1 commit forward (same shape)
+        "committed_speech_tokens_per_s_est": round(tok_s / 11.0, 1),
         "projection_tflops": round(proj_flops / (ms * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": "gemm_kernel<swiglu> (gate/up + SiLU*up, M=%d N=%d K=%d)" % (N, 2 * F, D),
+        "roofline": {"kernel": "gemm_dl_kernel<swiglu> (gate/up + SiLU*up, M=%d N=%d K=%d)" % (N, 2 * F, D),
                      "bound": "mfma", "achieved": round(tf_swiglu, 1), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tf_swiglu / BF16_PEAK_TFLOPS, 4), "traffic": traffic},
+                     "unit": "TFLOP/s", "frac": round(tf_swiglu / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "peak_measured": round(peak_meas, 1), "frac_of_measured": round(tf_swiglu / peak_meas, 4)},
         "kernels": {
             "attention": {"us": round(ms_attn * 1e3, 1), "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4)},
@@ -211,6 +237,104 @@ def main():
 
 
 COPY_BYTES = 1 << 30
+
+
+def measured_mfma_peak(dev):
+    """Sustained bf16 MFMA TFLOP/s of the register-only calibration kernel
+    (8 waves per SIMD, 2000 rounds of 8 independent 32x32x16 MFMAs)."""
+    from yapd_amd import kernels
+    blocks, iters = 2048, 2000
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flops = kernels.mfma_peak_probe(blocks, iters, out)
+    ms = time_launches(lambda: kernels.mfma_peak_probe(blocks, iters, out), 5, dev)
+    return flops / (ms * 1e-3) / 1e12
+
+
+def attn_stress(args, dev):
+    """30 layers of block attention back to back: 256 sequences, prefixes
+    round(exp(U[ln 64, ln 2048])), block 16, 16 x 64 heads; each layer's pages
+    are distinct random pages of its own 65,536-page pool (4 GiB per layer).
+    Only the referenced pages are filled (N(0, 1) bf16)."""
+    import numpy as np
+    from yapd_amd.paged import AttnPlan
+    from yapd_amd.synthetic import log_uniform_lengths
+    rows, bl, H, n_pages, L = 256, 16, 16, 65536, args.layers
+    lengths = log_uniform_lengths(rows, 64, 2048, seed=args.seed)
+    kv_len = [x + bl for x in lengths]
+    ppr = (max(kv_len) + 15) // 16
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    used = [(k + 15) // 16 for k in kv_len]
+    n_used = sum(used)
+    fill = torch.randn(n_used, 2, H, 1024, generator=g, device=dev).to(torch.bfloat16)
+    pools, tables = [], []
+    for layer in range(L):
+        perm = np.random.default_rng(args.seed * 1000 + layer).permutation(n_pages)[: rows * ppr]
+        table = torch.from_numpy(perm.reshape(rows, ppr).astype(np.int32)).to(dev)
+        pool = torch.empty(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
+        idx = torch.cat([table[r, :u] for r, u in enumerate(used)]).long()
+        pool.index_copy_(0, idx, fill)
+        pools.append(pool)
+        tables.append(table)
+    del fill
+    q = torch.randn(rows, bl, H, 64, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    plan = AttnPlan(kv_len, bl, H, dev)
+    torch.cuda.synchronize(dev)
+
+    def all_layers():
+        for layer in range(L):
+            plan.run(q, pools[layer], tables[layer], out, 0.125)
+    ms = time_launches(all_layers, max(args.steps // 4, 3), dev)
+    byts = L * (sum(kv_len) * H * 64 * 2 * 2 + 2 * rows * bl * H * 64 * 2 + n_used * 4)
+    gbs = byts / (ms * 1e-3) / 1e9
+    log(f"attention stress: {L} layers {ms:.3f} ms, {gbs:.0f} GB/s")
+    print(json.dumps({
+        "metric": "block attention HBM GB/s, 30 layers back to back (attention stress)", "value": round(gbs, 1),
+        "unit": "GB/s", "n_gpus": 1, "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic (N(0,1) K/V/q, random distinct pages)",
+        "config": {"workload": "paged block attention", "sequences": rows, "block": bl, "heads": H,
+                   "prefix_len": "round(exp(U[ln64, ln2048]))", "pool_pages_per_layer": n_pages, "layers": L,
+                   "kv_positions_per_layer": sum(kv_len)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": byts // L}}), flush=True)
+
+
+def quant_projections(args, dev):
+    """The four projections of 30 layers (qkv 3072x1024, o 1024x1024, gate/up
+    8192x1024, down 1024x4096) as 4-bit and 8-bit affine-quantised GEMMs
+    (group 64, MLX layout, fp16 scales/biases) at M = 8192; weights N(0, 0.02)."""
+    from yapd_amd.quant import qgemm_affine, quantize_affine
+    M, L = 8192, args.layers
+    shapes = [(3072, 1024), (1024, 1024), (8192, 1024), (1024, 4096)]
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    A = {k: torch.randn(M, k, generator=g, device=dev).to(torch.bfloat16) for k in (1024, 4096)}
+    outs = {n: torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n, _ in shapes}
+    flops = 2.0 * M * sum(n * k for n, k in shapes) * L
+    res = {}
+    for bits in (4, 8):
+        layers = [[quantize_affine(torch.randn(n, k, generator=g, device=dev) * 0.02, bits) for n, k in shapes]
+                  for _ in range(L)]
+        torch.cuda.synchronize(dev)
+
+        def all_layers():
+            for lw in layers:
+                for (n, k), (pk, sc, bi) in zip(shapes, lw):
+                    qgemm_affine(A[k], pk, sc, bi, bits, out=outs[n])
+        ms = time_launches(all_layers, 5, dev)
+        res[bits] = (ms, flops / (ms * 1e-3) / 1e12)
+        log(f"quant {bits}-bit: {L} layers {ms:.3f} ms, {res[bits][1]:.0f} TF/s")
+        del layers
+    ms4, tf4 = res[4]
+    print(json.dumps({
+        "metric": "affine-quantised projection TFLOP/s, 30 layers at M=8192", "value": round(tf4, 1),
+        "unit": "TFLOP/s", "n_gpus": 1, "ms_per_step": round(ms4, 4), "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic (weights N(0,0.02) quantised; A N(0,1))",
+        "config": {"workload": "qkv/o/gate-up/down dequant GEMMs", "M": M, "layers": L, "group": 64,
+                   "bits": 4},
+        "bits8": {"ms": round(res[8][0], 4), "tflops": round(res[8][1], 1),
+                  "frac": round(res[8][1] / BF16_PEAK_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(tf4, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf4 / BF16_PEAK_TFLOPS, 4)}}), flush=True)
 
 
 def kernel_sample(dev, N):

@@ -1,0 +1,22 @@
+/* Calibration kernel for the measurement harness (not part of the engine
+ * boundary; it has no counterpart in the reference).
+ *
+ * yapd_mfma_peak_probe: `blocks` workgroups of 4 waves each run `iters`
+ * rounds of 8 independent v_mfma_f32_32x32x16_bf16 on register operands and
+ * store one float per thread to out[blocks * 256].  Work per call:
+ * blocks * 4 * iters * 8 * 32768 flops; the sustained bf16 MFMA rate is that
+ * divided by the launch time. */
+#ifndef YAPD_PROBE_H
+#define YAPD_PROBE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int yapd_mfma_peak_probe(int blocks, int iters, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

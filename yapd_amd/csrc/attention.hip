@@ -100,15 +100,26 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
   // ends up holding keys 8g .. 8g+7 of the chunk.
   const int key_t0 = 8 * (n >> 2) + (n & 3);
 
-  for (int k0 = kb; k0 < ke; k0 += kChunk) {
-    const int pi0 = min(k0 / kPageSize, last_page);
-    int64_t p0 = tab[pi0];
-    int64_t p1 = tab[min(pi0 + 1, last_page)];
-    p0 = min(max(p0, int64_t{0}), P.n_pages - 1);  // a bad table entry cannot fault
-    p1 = min(max(p1, int64_t{0}), P.n_pages - 1);
-
-    // K fragments (A operand of S^T): tile t row n -> key key_t0 + 4t.
-    u32x4_t kf[2][2];
+  // The row's page ids, 64 at a time: lane i holds the page of table column
+  // tab_base + i (clamped), and a chunk picks its two with readlane, so the
+  // K/V loads never wait on a page-table load inside the loop.
+  int tab_base = -1;
+  int tabv = 0;
+  auto page_of = [&](int pi) -> int64_t {
+    pi = min(pi, last_page);
+    if (pi - tab_base >= 64 || tab_base < 0) {  // uniform: pi is the same for the wave
+      tab_base = pi;
+      tabv = tab[min(tab_base + lane, last_page)];
+    }
+    const int64_t pg = __builtin_amdgcn_readlane(tabv, pi - tab_base);
+    return min(max(pg, int64_t{0}), P.n_pages - 1);  // a bad table entry cannot fault
+  };
+  // K fragments (A operand of S^T): tile t row n -> key key_t0 + 4t.
+  // V^T fragments (A operand of O^T): row hd = 16mt + n, keys 8g .. 8g+7.
+  auto load_chunk = [&](int k0, u32x4_t (&kf)[2][2], u32x4_t (&vf)[4]) {
+    const int pi0 = k0 / kPageSize;
+    const int64_t p0 = page_of(pi0);
+    const int64_t p1 = page_of(pi0 + 1);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int key = key_t0 + 4 * t;
@@ -117,14 +128,17 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
       kf[t][0] = load16(kp);
       kf[t][1] = load16(kp + 32);
     }
-    // V^T fragments (A operand of O^T): row hd = 16mt + n, keys 8g .. 8g+7.
-    u32x4_t vf[4];
-    {
-      const int64_t pg = g < 2 ? p0 : p1;
-      const uint16_t* vp = P.pool + v_offset(pg, h, H, 8 * (g & 1), n);
+    const int64_t pg = g < 2 ? p0 : p1;
+    const uint16_t* vp = P.pool + v_offset(pg, h, H, 8 * (g & 1), n);
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) vf[mt] = load16(vp + 16 * mt * kPageSize);
-    }
+    for (int mt = 0; mt < 4; ++mt) vf[mt] = load16(vp + 16 * mt * kPageSize);
+  };
+
+  // Chunk k0 + 32 is loaded while chunk k0 is multiplied.
+  u32x4_t kf[2][2], vf[4], kn[2][2], vn[4];
+  if (kb < ke) load_chunk(kb, kf, vf);
+  for (int k0 = kb; k0 < ke; k0 += kChunk) {
+    if (k0 + kChunk < ke) load_chunk(k0 + kChunk, kn, vn);
     const bool tail = k0 + kChunk > kvl;
     const int diag0 = kvl - bl;  // causal: query q may see keys <= diag0 + q
     const bool mask_chunk = tail || (P.causal && k0 + kChunk > diag0 + 1);
@@ -193,6 +207,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
         o[qt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vf[mt]), pf, o[qt][mt], 0, 0, 0);
       }
     }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      kf[t][0] = kn[t][0];
+      kf[t][1] = kn[t][1];
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) vf[mt] = vn[mt];
   }
 
   // o[qt][mt][j] = O^T[hd = 16mt + 4g + j][q = qt*16 + n]

@@ -77,6 +77,7 @@ struct GemmParams {
   int64_t ldq;  // uint32 words per row
   const uint16_t* qscale;
   const uint16_t* qbias;
+  int xcd_band;  // 1: XCD-banded tile order (set by the launcher)
 };
 
 __device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
@@ -299,6 +300,23 @@ __device__ __forceinline__ uint32_t dq_pair(uint32_t word, int shift, float sc, 
   return pack_bf16x2(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
 }
 
+// XCD-aware tile order for single-round grids (at most one workgroup per
+// CU).  Workgroups are dispatched round-robin over the 8 XCDs (linear id L
+// runs on XCD L % 8), each with its own L2.  In row-major order the column
+// tiles of one A row block land on different XCDs, so every one of them
+// fetches that block; with `band` set, XCD j instead takes the band of row
+// tiles [j R/8, (j+1) R/8) across all column tiles, and each A row block is
+// fetched into one L2.  (For multi-round grids the row-major order measured
+// faster and is kept.)
+__device__ __forceinline__ int2 tile_coords(int xcd_band) {
+  const int C = gridDim.x, R = gridDim.y;
+  const int L = blockIdx.x + C * blockIdx.y;
+  if (!xcd_band || R % 8 != 0) return make_int2(blockIdx.x, blockIdx.y);
+  const int band = R / 8;
+  const int j = L % 8, i = L / 8;
+  return make_int2(i / band, j * band + i % band);  // (column tile, row tile)
+}
+
 // Epilogue dispatch.  Every wave has finished reading the LDS stages (the
 // main loop ends with a barrier and no LDS reads after it), so the epilogues
 // may reuse all of LDS.
@@ -326,7 +344,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // wave index: uniform
   const int wm = wave / T::WN, wn = wave % T::WN;
-  const int m0 = blockIdx.y * T::BM, n0 = blockIdx.x * T::BN;
+  const int2 tc = tile_coords(p.xcd_band);
+  const int m0 = tc.y * T::BM, n0 = tc.x * T::BN;
 
   // Global -> register staging: CA (CB) chunks of 16 bytes per thread.  Rows
   // past M (N) re-read the last valid row: they only feed accumulator rows
@@ -531,7 +550,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // wave index: uniform
   const int wm = wave / T::WN, wn = wave % T::WN;
-  const int m0 = blockIdx.y * T::BM, n0 = blockIdx.x * T::BN;
+  const int2 tc = tile_coords(p.xcd_band);
+  const int m0 = tc.y * T::BM, n0 = tc.x * T::BN;
 
   // Per-lane sources of this wave's LA + LB loads (k offset added per tile).
   // Rows past M (N) re-read the last valid row, as in the staged kernel.
@@ -735,14 +755,30 @@ int launch_dl(const GemmParams& p, hipStream_t st) {
 
 using TileD = Tile<256, 256, BK, 2, 4>;  // direct-load large tile
 
+// Compute units of the current device (cached per device id).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int EPI, int AM, int BQ = 0>
-int launch_gemm(const GemmParams& p, hipStream_t st) {
+int launch_gemm(GemmParams p, hipStream_t st) {
   // Large tiles once they still give at least one workgroup per CU.
   const int64_t big_tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
   if (big_tiles >= 256) {
+    p.xcd_band = big_tiles <= cu_count() ? 1 : 0;
     if constexpr (BQ == 0) return launch_dl<TileD, EPI, AM>(p, st);
     return launch_tile<TileL, EPI, AM, BQ>(p, st);
   }
+  const int64_t small_tiles = static_cast<int64_t>((p.M + 127) / 128) * ((p.N + 127) / 128);
+  p.xcd_band = small_tiles <= cu_count() ? 1 : 0;
   return launch_tile<TileS, EPI, AM, BQ>(p, st);
 }
 
