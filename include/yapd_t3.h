@@ -221,6 +221,27 @@ int yapd_t3_block_forward(const yapd_t3_model* model, const yapd_t3_workspace* w
                           void* hidden_out, const void* head_w, int vocab, const void* shift_ctx, void* logits,
                           int64_t ld_logits, void* stream);
 
+/* ------------------------------------------------------------------------ *
+ * Continuous-batching tick bookkeeping (server/engine.py:522-612, the state
+ * updates of FlashEngine._step_gpu after the scorer).  For slots s <
+ * n_slots, with commit = is_commit[s] on entry:
+ *   xt_final[s][j] = commit ? xt_blk[s][j] : xt_new[s][j], scattered into
+ *   xt[s][blk_start[s] + j];  n_mask_after / hit_eos over xt_final;
+ *   k_step    = commit ? 0 : k_step + 1;
+ *   cache_len = commit ? min(cache_len + bl, max_len - bl) : cache_len;
+ *   blk_start = commit ? min(blk_start + bl, n_max - bl) : blk_start;
+ *   is_commit = !commit && !hit_eos && (n_mask_after == 0 || k_step >= K);
+ *   flags[s] = {commit, n_mask_after, hit_eos, k_step, blk_start, n_speech};
+ *   the n_branch shift_ctx rows of a committing slot take the block's last
+ *   hidden row (server/engine.py:522-527).
+ * hidden [n_slots * n_branch * bl, D] and shift_ctx [n_slots * n_branch, D]
+ * are bf16; every other array is int64 except is_commit (uint8). */
+int yapd_tick_update(int n_slots, int bl, int n_branch, int D, int K, int64_t mask_id, int64_t stop_id,
+                     int64_t max_len, int64_t n_max, int64_t* xt, int64_t xt_stride, const int64_t* xt_blk,
+                     const int64_t* xt_new, int64_t* k_step, int64_t* cache_len, int64_t* blk_start,
+                     uint8_t* is_commit, const int64_t* n_speech, const void* hidden, void* shift_ctx,
+                     int64_t* flags, int64_t* xt_final, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

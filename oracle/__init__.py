@@ -22,4 +22,6 @@ Modules (each function cites the reference file:line it restates):
   (engines/flashinfer.py:1452-1461).
 * :mod:`oracle.quant` -- MLX affine group quantisation (engines/mlx.py:221-255
   calls ``mlx.nn.quantize``; the documented MLX formula is restated).
+* :mod:`oracle.serve` -- the continuous-batching tick bookkeeping of
+  server/engine.py:522-620 (commit / denoise transitions, clamps, flags).
 """

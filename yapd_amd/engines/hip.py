@@ -239,13 +239,22 @@ class HipEngine:
             kernels.ptr(getattr(plan, "counts", None)), kernels.ptr(plan.part_o), kernels.ptr(plan.part_ml),
             int(plan.n_slots))
 
+    def _descriptor(self, row0: int) -> "kernels.T3Model":
+        """The native model descriptor whose batch row 0 is page-table row ``row0``."""
+        if row0 == 0:
+            return self._c_model
+        m = kernels.T3Model.from_buffer_copy(self._c_model)
+        m.page_table = self._kv.table.data_ptr() + row0 * self._kv.table.stride(0) * self._kv.table.element_size()
+        return m
+
     def _run(self, buf: _Buffers, plan, kv_len_dev: Tensor, *, causal: bool = False,
              head_w: Optional[Tensor] = None, shift_ctx: Optional[Tensor] = None,
-             logits: Optional[Tensor] = None) -> None:
+             logits: Optional[Tensor] = None, row0: int = 0) -> None:
         ws = self._workspace(buf, plan)
         V = 0 if head_w is None else int(head_w.shape[0])
+        c_model = self._descriptor(row0)
         kernels.check(kernels.load_library().yapd_t3_block_forward(
-            ctypes.byref(self._c_model), ctypes.byref(ws), buf.emb.data_ptr(), buf.rows, buf.bl,
+            ctypes.byref(c_model), ctypes.byref(ws), buf.emb.data_ptr(), buf.rows, buf.bl,
             buf.pos0.data_ptr(), kv_len_dev.data_ptr(), int(causal), buf.hidden.data_ptr(),
             kernels.ptr(head_w), V, kernels.ptr(shift_ctx), kernels.ptr(logits),
             0 if logits is None else logits.stride(1), kernels.stream_ptr(self._device)))
@@ -269,31 +278,50 @@ class HipEngine:
             if t.size(0) not in (1, B):
                 raise ValueError(f"prefix batch {t.size(0)} must be 1 or engine batch {B}")
             embs = [t[min(i, t.size(0) - 1)] for i in range(B)]
+        sos = self._prefill(0, embs)
         lps = [int(e.shape[0]) for e in embs]
-        if max(lps) > self._max_seq_len:
-            raise ValueError("prefix longer than max_seq_len")
+        self._cache_lens = list(lps)
+        self._prefix_lens = list(lps)
+        return sos
+
+    def prefix_forward_rows(self, row0: int, embs: List[Tensor]) -> Tensor:
+        """Prefill only rows ``[row0, row0 + len(embs))`` (their KV pages); the other rows and
+        their caches are untouched.  Returns those rows' SOS hidden ``(n, 1, D)``."""
+        n = len(embs)
+        if not 1 <= n or row0 < 0 or row0 + n > self._batch_size:
+            raise ValueError(f"rows [{row0}, {row0 + n}) outside the engine batch {self._batch_size}")
+        embs = [e.reshape(-1, self._hidden) for e in embs]
+        sos = self._prefill(row0, embs)
+        for i, e in enumerate(embs):
+            self._cache_lens[row0 + i] = self._prefix_lens[row0 + i] = int(e.shape[0])
+        return sos
+
+    def _prefill(self, row0: int, embs: List[Tensor]) -> Tensor:
+        """Causal forward of ragged prefixes in 64-token chunks on batch rows row0..; pad tokens
+        only write KV past each row's prefix (overwritten by later blocks, never attended)."""
+        n, D = len(embs), self._hidden
+        lps = [int(e.shape[0]) for e in embs]
+        if min(lps) < 1 or max(lps) > self._max_seq_len:
+            raise ValueError("prefix length must be in [1, max_seq_len]")
         lp_max = max(lps)
-        sos = torch.empty(B, 1, D, dtype=self._dtype, device=self._device)
-        done = [False] * B
+        sos = torch.empty(n, 1, D, dtype=self._dtype, device=self._device)
+        done = [False] * n
         for c0 in range(0, lp_max, PREFILL_CHUNK):
             bl = min(PREFILL_CHUNK, lp_max - c0)
-            buf = self._buffers(B, bl)
+            buf = self._buffers(n, bl)
             buf.emb.zero_()
             for r, e in enumerate(embs):
-                n = max(0, min(bl, lps[r] - c0))
-                if n > 0:
-                    buf.emb[r * bl: r * bl + n].copy_(e[c0: c0 + n].to(self._dtype))
+                k = max(0, min(bl, lps[r] - c0))
+                if k > 0:
+                    buf.emb[r * bl: r * bl + k].copy_(e[c0: c0 + k].to(self._dtype))
             buf.pos0.fill_(c0)
-            kv_len = [c0 + bl] * B
-            plan = self._plan(kv_len, bl)
-            self._run(buf, plan, plan.kv_len, causal=True)
-            hid = buf.hidden.view(B, bl, D)
-            for r in range(B):
+            plan = self._plan([c0 + bl] * n, bl)
+            self._run(buf, plan, plan.kv_len, causal=True, row0=row0)
+            hid = buf.hidden.view(n, bl, D)
+            for r in range(n):
                 if not done[r] and c0 <= lps[r] - 1 < c0 + bl:
                     sos[r, 0] = hid[r, lps[r] - 1 - c0]
                     done[r] = True
-        self._cache_lens = list(lps)
-        self._prefix_lens = list(lps)
         return sos
 
     # ------------------------------------------------------------------ #

@@ -49,6 +49,9 @@ _SIGNATURES = {
     "yapd_qgemm_affine": (c_int, [c_void, c_i64, c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_int,
                                   c_void, c_i64, c_void]),
     "yapd_mfma_peak_probe": (c_int, [c_int, c_int, c_void, c_void]),
+    "yapd_tick_update": (c_int, [c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_void, c_i64,
+                                 c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void,
+                                 c_void, c_void]),
     "yapd_t3_block_forward": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void, c_int, c_void,
                                       c_void, c_int, c_void, c_void, c_i64, c_void]),
 }
@@ -398,3 +401,35 @@ def mfma_peak_probe(blocks: int, iters: int, out: torch.Tensor) -> float:
     require(out.numel() >= blocks * 256, "out needs blocks * 256 floats")
     check(load_library().yapd_mfma_peak_probe(blocks, iters, out.data_ptr(), stream_ptr(out.device)))
     return float(blocks) * 4 * iters * 8 * 32768
+
+
+def tick_update(*, xt: torch.Tensor, xt_blk: torch.Tensor, xt_new: torch.Tensor, k_step: torch.Tensor,
+                cache_len: torch.Tensor, blk_start: torch.Tensor, is_commit: torch.Tensor, n_speech: torch.Tensor,
+                hidden: torch.Tensor, shift_ctx: torch.Tensor, flags: torch.Tensor, xt_final: torch.Tensor,
+                n_branch: int, K: int, mask_id: int, stop_id: int, max_len: int) -> None:
+    """Continuous-batching state update after the scorer (``yapd_tick_update``) for the first
+    ``xt_blk.shape[0]`` slots; every state tensor is updated in place."""
+    dev = xt.device
+    S, bl = xt_blk.shape
+    D = hidden.shape[-1]
+    for name, t in (("xt_blk", xt_blk), ("xt_new", xt_new), ("xt_final", xt_final)):
+        require_cuda(t, name, torch.int64, dev)
+        require(tuple(t.shape) == (S, bl), f"{name} must be [slots, bl]")
+    require_cuda(xt, "xt", torch.int64, dev, contiguous=False)
+    require(xt.dim() == 2 and xt.stride(1) == 1 and xt.shape[0] >= S, "xt must be [slots, n_max] row-major")
+    for name, t in (("k_step", k_step), ("cache_len", cache_len), ("blk_start", blk_start), ("n_speech", n_speech)):
+        require_cuda(t, name, torch.int64, dev)
+        require(t.numel() >= S, f"{name} needs one entry per slot")
+    require_cuda(is_commit, "is_commit", torch.uint8, dev)
+    require(is_commit.numel() >= S, "is_commit needs one entry per slot")
+    require_cuda(hidden, "hidden", torch.bfloat16, dev)
+    require(hidden.numel() >= S * n_branch * bl * D, "hidden must hold slots * n_branch * bl rows")
+    require_cuda(shift_ctx, "shift_ctx", torch.bfloat16, dev)
+    require(shift_ctx.numel() >= S * n_branch * D and shift_ctx.shape[-1] == D, "shift_ctx must be [rows, 1, D]")
+    require_cuda(flags, "flags", torch.int64, dev)
+    require(tuple(flags.shape) == (S, 6), "flags must be [slots, 6]")
+    check(load_library().yapd_tick_update(
+        S, bl, n_branch, D, K, mask_id, stop_id, max_len, xt.shape[1], xt.data_ptr(), xt.stride(0),
+        xt_blk.data_ptr(), xt_new.data_ptr(), k_step.data_ptr(), cache_len.data_ptr(), blk_start.data_ptr(),
+        is_commit.data_ptr(), n_speech.data_ptr(), hidden.data_ptr(), shift_ctx.data_ptr(), flags.data_ptr(),
+        xt_final.data_ptr(), stream_ptr(dev)))

@@ -50,6 +50,16 @@ class PagedKV:
     def bytes_per_layer(self) -> int:
         return self.pools[0].numel() * 2
 
+    def swap_rows(self, a: int, b: int) -> None:
+        """Exchange page-table rows ``a`` and ``b`` (host mirror and device table): each row's KV
+        moves with its pages, nothing is copied.  Device work is stream-ordered, no host sync."""
+        if a == b:
+            return
+        self.table_host[[a, b]] = self.table_host[[b, a]]
+        tmp = self.table[a].clone()
+        self.table[a].copy_(self.table[b])
+        self.table[b].copy_(tmp)
+
     def copy_row_pages(self, src_row: int, dst_row: int, n_positions: int) -> None:
         """Copy the pages holding positions ``[0, n_positions)`` of one row to another, every layer."""
         npg = (n_positions + PAGE_SIZE - 1) // PAGE_SIZE

@@ -111,8 +111,10 @@ class BlockScorer:
     def __call__(self, logits: torch.Tensor, xt_blk: torch.Tensor, k_step: torch.Tensor, *,
                  layout: str = "stacked", active: Optional[torch.Tensor] = None,
                  temperature: float = 0.0, position_noise: bool = False, seed: int = 0,
-                 rng_offset: int = 0) -> ScoreResult:
-        P = self.n_pairs
+                 rng_offset: int = 0, n_pairs: Optional[int] = None) -> ScoreResult:
+        """Score the first ``n_pairs`` pairs (default: all); outputs are ``[n_pairs, ...]`` views."""
+        P = self.n_pairs if n_pairs is None else int(n_pairs)
+        kernels.require(1 <= P <= self.n_pairs, f"n_pairs must be in [1, {self.n_pairs}]")
         if self.cfg > 0:
             if layout == "stacked":
                 row0, step, null_off = 0, 1, P
@@ -126,7 +128,7 @@ class BlockScorer:
             logits, n_pairs=P, cond_row0=row0, pair_row_step=step, null_row_offset=null_off,
             log_prior=self.log_prior, xt_blk=xt_blk, k_step=k_step, sched=self.sched, q_tab=self.q_t,
             cfg_w=self.cfg, quantile_on=self.tau > 0, mask_id=self.mask_id, stop_id=self.stop_id,
-            out=self.out, active=active, temperature=temperature,
+            out={k: v[:P] for k, v in self.out.items()}, active=active, temperature=temperature,
             pos_gumbel=position_noise, seed=seed, rng_offset=rng_offset)
-        o = self.out
+        o = {k: v[:P] for k, v in self.out.items()}
         return ScoreResult(o["sampled"], o["pmi"], o["unmask"], o["xt_out"], o["n_mask_after"], o["hit_eos"])
