@@ -19,6 +19,10 @@ around single launches on the stream the kernel runs on, right after the
 timed region.  ``cpu_baseline`` times the oracle (torch on the host cores) on
 a bounded sample of the same step.
 
+``--workload serve`` runs the continuous-batching engine (server defaults:
+128 slots, block 16, K = 10, temperature 0.6, position temperature 5, CFG 1)
+over a queue of requests and reports committed speech tokens per second.
+
 ``--workload attn_stress`` instead measures 30 layers of block attention
 back to back over 256 sequences with log-uniform [64, 2048] prefixes, block
 16, each layer's pages drawn at random from its own 65,536-page pool; and
@@ -55,7 +59,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["step", "attn_stress", "quant"], default="step")
+    ap.add_argument("--workload", choices=["step", "attn_stress", "quant", "serve"], default="step")
+    ap.add_argument("--requests", type=int, default=384, help="serve workload: number of requests")
     ap.add_argument("--kernel-sample", action="store_true",
                     help="only run the dominant GEMM (bench shape) and a 1 GiB copy, for rocprofv3 --pmc")
     return ap.parse_args()
@@ -102,6 +107,9 @@ def main():
         return
     if args.workload == "quant":
         quant_projections(args, dev)
+        return
+    if args.workload == "serve":
+        serve(args, dev)
         return
     B = 2 * Bp
     D, H, F, V = 1024, 16, 4096, 8194
@@ -297,6 +305,64 @@ def attn_stress(args, dev):
                    "kv_positions_per_layer": sum(kv_len)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": byts // L}}), flush=True)
+
+
+def serve(args, dev):
+    """Continuous batching (server/engine.py FlashEngine defaults): 128 slots, block 16,
+    K = 10 denoise steps, temperature 0.6, position temperature 5.0, CFG 1.0, tau 0.1;
+    requests with prefixes U[100, 300] and speech budgets of 208 tokens (13 blocks)
+    arrive all at once; the timed window runs from the first tick to the last commit."""
+    from yapd_amd.serve import HipFlashEngine, Request
+    from yapd_amd.synthetic import MASK_ID, SOS_ID, STOP_ID, make_t3, uniform_lengths
+    L, n_req, n_speech = args.layers, args.requests, 208
+    model = make_t3(n_layers=L, seed=args.seed, device=dev)
+    V = model.speech_head.weight.shape[0]
+    g = torch.Generator().manual_seed(args.seed + 1)
+    prior = torch.distributions.Dirichlet(torch.full((V,), 0.1)).sample()
+    log_prior = prior.clamp_min(1e-8).log()
+    eng = HipFlashEngine(model, log_prior=log_prior, mask_id=MASK_ID, stop_id=STOP_ID, codec_vocab=SOS_ID,
+                         max_active=128, max_prefix_tokens=320, max_speech_tokens=624, num_steps=10,
+                         temperature=0.6, time_shift_tau=0.1, omnivoice_t_shift=0.5, cfg_scale=1.0,
+                         position_temperature=5.0, prefill_max=16, block_size=16, page_table_seed=args.seed + 2)
+    sos = model.speech_emb.weight[SOS_ID].detach().to(torch.bfloat16)
+    lens = uniform_lengths(n_req, 100, 300, seed=args.seed + 3)
+    reqs = []
+    for i, lp in enumerate(lens):
+        pre = (torch.randn(lp, model.speech_emb.weight.shape[1], generator=g) * 0.5).to(dev, torch.bfloat16)
+        pre[-1] = sos
+        reqs.append(Request(rid=i, prefix=pre, n_speech=n_speech))
+    # warm-up: a few requests through the same engine (buffers, plans)
+    for r in reqs[:8]:
+        eng.submit(r)
+    eng.run_until_idle()
+    torch.cuda.synchronize(dev)
+    eng.finished.clear()
+    eng.commit_blocks = 0
+    t0_tick = eng.tick_id
+    t0 = time.perf_counter()
+    for r in reqs[8:]:
+        eng.submit(r)
+    eng.run_until_idle()
+    torch.cuda.synchronize(dev)
+    secs = time.perf_counter() - t0
+    done = [r for r in reqs[8:] if r.t3_done]
+    toks = sum(len(r.committed) for r in done)
+    ticks = eng.tick_id - t0_tick
+    ttfc = sorted(r.t_first_commit - r.t_recv for r in done if r.t_first_commit > 0)
+    log(f"serve: {len(done)} requests, {toks} committed tokens in {secs:.2f} s over {ticks} ticks "
+        f"({secs / max(ticks, 1) * 1e3:.2f} ms/tick)")
+    print(json.dumps({
+        "metric": "committed speech tokens/sec, continuous batching (128 slots, 30 layers)",
+        "value": round(toks / secs, 1), "unit": "committed speech tokens/s", "n_gpus": 1,
+        "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic (seeded random-init T3 weights, random prefixes, Dirichlet(0.1) prior)",
+        "config": {"workload": "continuous-batching decode (admission, denoise, commit, retirement)",
+                   "requests": len(done), "slots": 128, "block": 16, "K": 10, "layers": L,
+                   "prefix_len": "U[100,300]", "n_speech": n_speech, "temperature": 0.6,
+                   "position_temperature": 5.0, "cfg_w": 1.0},
+        "ticks": ticks, "ms_per_tick": round(secs / max(ticks, 1) * 1e3, 3),
+        "ttfc_s_median": round(ttfc[len(ttfc) // 2], 3) if ttfc else None,
+        "commit_blocks": eng.commit_blocks}), flush=True)
 
 
 def quant_projections(args, dev):
