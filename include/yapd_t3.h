@@ -127,6 +127,12 @@ int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, c
 int yapd_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, int M, int N, int K, void* C,
                    int64_t ldc, void* stream);
 
+/* Projection into the residual stream: residual = bf16(residual + bf16(A*W^T))
+ * (o_proj / down_proj + the residual add of fused_add_rmsnorm,
+ * engines/flashinfer.py:1040-1060; the norm itself is yapd_rmsnorm). */
+int yapd_gemm_bf16_residual(const void* A, int64_t lda, const void* W, int64_t ldw, int M, int N, int K,
+                            void* residual, int64_t ld_res, void* stream);
+
 /* Fused QKV + NeoX RoPE + paged KV write (engines/flashinfer.py:998-1035):
  * rows r*bl+j at position pos0[r]+j; cos/sin fp32 [max_pos, 64] hold the
  * model-dtype table (flashinfer.py:246-255) in HF's cat(freqs, freqs)

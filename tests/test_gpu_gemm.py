@@ -36,6 +36,20 @@ def test_gemm_bf16(dev, M, N, K):
     assert rel_err(out.cpu(), ref) <= 8e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(200, 1024, 1024), (16384 // 8, 1024, 4096), (4100, 1024, 1024)])
+def test_gemm_residual_equals_separate_add(dev, M, N, K):
+    """The fused residual add is bit-identical to the projection stored in bf16
+    followed by the bf16 residual add (HF's two roundings)."""
+    A = rnd(M, K, seed=21).to(dev)
+    W = rnd(N, K, std=0.02, seed=22).to(dev)
+    res0 = rnd(M, N, seed=23).to(dev) * 4
+    delta = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    kernels.gemm_bf16(A, W, delta)
+    res = res0.clone()
+    kernels.gemm_bf16_residual(A, W, res)
+    assert torch.equal(res.cpu(), (res0 + delta).cpu())
+
+
 def test_gemm_padded_ldc_and_strided_a(dev):
     M, N, K = 96, 300, 256
     base = rnd(M, K + 64, seed=3).to(dev)

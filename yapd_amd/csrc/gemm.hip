@@ -46,7 +46,7 @@ struct Tile {
 };
 constexpr int BK = 64;  // K granularity every config shares
 
-enum EpiMode { kEpiStore = 0, kEpiQkv = 1, kEpiSwiglu = 2 };
+enum EpiMode { kEpiStore = 0, kEpiQkv = 1, kEpiSwiglu = 2, kEpiResidual = 3 };
 enum AMode { kAPlain = 0, kAShift = 1 };
 
 struct GemmParams {
@@ -253,8 +253,11 @@ __device__ __forceinline__ void epilogue_swiglu(const GemmParams& p, const f32x1
 
 // Plain-store epilogue through LDS: the waves park their bf16 tile in the
 // (now idle) LDS staging area, then every thread writes whole 16-byte row
-// chunks, instead of one 2-byte store per accumulator.
-template <class T>
+// chunks, instead of one 2-byte store per accumulator.  With ADD the tile is
+// the residual branch's delta: C = bf16(C + bf16(acc)), the decoder layer's
+// residual add (HF LlamaDecoderLayer; engines/flashinfer.py:1040-1060) with
+// the reference's two roundings (the fp32 sum of two bf16 values is exact).
+template <class T, bool ADD = false>
 __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
                                                    uint16_t* lds, int m0, int n0, int wm, int wn, int lane, int tid) {
   constexpr int CP = T::BN + 8;  // staging row pitch (bf16)
@@ -281,9 +284,21 @@ __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f3
     const uint16_t* src = lds + r * CP + cc;
     uint16_t* dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
     if (vec_ok && n + 8 <= p.N) {
-      *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
+      if constexpr (ADD) {
+        const u32x4_t r = *reinterpret_cast<const u32x4_t*>(dst);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v[w] = pack_bf16x2(bf16lo(r[w]) + bf16lo(v[w]), bf16hi(r[w]) + bf16hi(v[w]));
+      }
+      *reinterpret_cast<u32x4_t*>(dst) = v;
     } else {
-      for (int t = 0; t < 8 && n + t < p.N; ++t) dst[t] = src[t];
+      for (int t = 0; t < 8 && n + t < p.N; ++t) {
+        if constexpr (ADD) {
+          dst[t] = static_cast<uint16_t>(f32_to_bf16(bf16_to_f32(dst[t]) + bf16_to_f32(src[t])));
+        } else {
+          dst[t] = src[t];
+        }
+      }
     }
   }
 }
@@ -325,6 +340,8 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, const f32x16_t 
                                             const RowMeta& rm, int m0, int n0, int wm, int wn, int lane, int tid) {
   if constexpr (EPI == kEpiStore) {
     store_tile_via_lds<T>(p, acc, lds, m0, n0, wm, wn, lane, tid);
+  } else if constexpr (EPI == kEpiResidual) {
+    store_tile_via_lds<T, true>(p, acc, lds, m0, n0, wm, wn, lane, tid);
   } else if constexpr (EPI == kEpiSwiglu) {
     epilogue_swiglu<T>(p, acc, lds, m0, n0, wm, wn, lane, tid);
   } else {
@@ -812,6 +829,23 @@ extern "C" int yapd_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t
   if (int rc = yapd::check_common(p)) return rc;
   YAPD_REQUIRE(C != nullptr && ldc >= N, "gemm: bad C");
   return yapd::launch_gemm<yapd::kEpiStore, yapd::kAPlain>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int yapd_gemm_bf16_residual(const void* A, int64_t lda, const void* W, int64_t ldw, int M, int N, int K,
+                                       void* residual, int64_t ld_res, void* stream) {
+  GemmParams p{};
+  p.A = static_cast<const uint16_t*>(A);
+  p.lda = lda;
+  p.W = static_cast<const uint16_t*>(W);
+  p.ldw = ldw;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.C = static_cast<uint16_t*>(residual);
+  p.ldc = ld_res;
+  if (int rc = yapd::check_common(p)) return rc;
+  YAPD_REQUIRE(residual != nullptr && ld_res >= N, "gemm_residual: bad residual");
+  return yapd::launch_gemm<yapd::kEpiResidual, yapd::kAPlain>(p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int yapd_gemm_head_shift(const void* hidden, const void* shift_ctx, int rows, int bl, int K,

@@ -4,10 +4,10 @@
 // goes to the caller's stream, so the whole call can be captured in a HIP
 // graph.
 //
-// Per layer:  qkv+rope+kv-write GEMM -> paged attention -> o_proj GEMM ->
-//             residual add + post-attention RMSNorm -> gate/up+SiLU GEMM ->
-//             down GEMM -> residual add + next input RMSNorm (final norm
-//             after the last layer).
+// Per layer:  qkv+rope+kv-write GEMM -> paged attention -> o_proj GEMM
+//             adding into the residual -> post-attention RMSNorm ->
+//             gate/up+SiLU GEMM -> down GEMM adding into the residual ->
+//             next input RMSNorm (final norm after the last layer).
 #include "common.h"
 
 #define YAPD_TRY(expr)            \
@@ -40,14 +40,14 @@ extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_works
     YAPD_TRY(yapd_attn_paged_block(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols,
                                    kv_len, rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts,
                                    ws->part_o, ws->part_ml, ws->n_slots, scale, causal, ws->attn, st));
-    YAPD_TRY(yapd_gemm_bf16(ws->attn, HD, L.w_o, HD, M, D, HD, ws->delta, D, st));
-    YAPD_TRY(yapd_rmsnorm(ws->delta, res, nullptr, L.ln_post, L.eps_post, M, D, xn, st));
+    YAPD_TRY(yapd_gemm_bf16_residual(ws->attn, HD, L.w_o, HD, M, D, HD, res, D, st));
+    YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, L.ln_post, L.eps_post, M, D, xn, st));
     YAPD_TRY(yapd_gemm_swiglu(xn, D, L.w_gate_up, M, F, D, ws->act, F, st));
-    YAPD_TRY(yapd_gemm_bf16(ws->act, F, L.w_down, F, M, D, F, ws->delta, D, st));
+    YAPD_TRY(yapd_gemm_bf16_residual(ws->act, F, L.w_down, F, M, D, F, res, D, st));
     const bool last = li + 1 == m->n_layers;
     const void* wn = last ? m->final_norm : m->layers[li + 1].ln_in;
     const float eps = last ? m->final_eps : m->layers[li + 1].eps_in;
-    YAPD_TRY(yapd_rmsnorm(ws->delta, res, nullptr, wn, eps, M, D, last ? hidden_out : xn, st));
+    YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, wn, eps, M, D, last ? hidden_out : xn, st));
   }
   if (head_w != nullptr) {
     YAPD_REQUIRE(shift_ctx && logits && vocab >= 1, "t3_block_forward: head needs shift_ctx and logits");

@@ -40,6 +40,7 @@ _SIGNATURES = {
                               c_int, c_int, c_void]),
     "yapd_kv_gather": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_void]),
     "yapd_gemm_bf16": (c_int, [c_void, c_i64, c_void, c_i64, c_int, c_int, c_int, c_void, c_i64, c_void]),
+    "yapd_gemm_bf16_residual": (c_int, [c_void, c_i64, c_void, c_i64, c_int, c_int, c_int, c_void, c_i64, c_void]),
     "yapd_gemm_head_shift": (c_int, [c_void, c_void, c_int, c_int, c_int, c_void, c_i64, c_int, c_void, c_i64,
                                      c_void]),
     "yapd_gemm_swiglu": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_i64, c_void]),
@@ -306,6 +307,19 @@ def gemm_bf16(A: torch.Tensor, W: torch.Tensor, out: torch.Tensor) -> None:
     require(W.shape[1] == K and tuple(out.shape) == (M, N), "gemm shapes")
     check(load_library().yapd_gemm_bf16(A.data_ptr(), A.stride(0), W.data_ptr(), W.stride(0), M, N, K,
                                         out.data_ptr(), out.stride(0), stream_ptr(dev)))
+
+
+def gemm_bf16_residual(A: torch.Tensor, W: torch.Tensor, residual: torch.Tensor) -> None:
+    """``residual = bf16(residual + bf16(A @ W^T))`` in place (projection + residual add)."""
+    dev = A.device
+    _mat(A, "A", dev)
+    _mat(W, "W", dev)
+    _mat(residual, "residual", dev)
+    M, K = A.shape
+    N = W.shape[0]
+    require(W.shape[1] == K and tuple(residual.shape) == (M, N), "gemm shapes")
+    check(load_library().yapd_gemm_bf16_residual(A.data_ptr(), A.stride(0), W.data_ptr(), W.stride(0), M, N, K,
+                                                 residual.data_ptr(), residual.stride(0), stream_ptr(dev)))
 
 
 def gemm_head_shift(hidden: torch.Tensor, shift_ctx: torch.Tensor, W: torch.Tensor, logits: torch.Tensor) -> None:
