@@ -57,7 +57,7 @@ int yapd_abi_version(void);
  * pos_gumbel != 0 adds standard Gumbel noise to masked PMI
  * (server/engine.py:559-561; the reference adds it unscaled).
  * Outputs [n_pairs, bl]: sampled (int64), pmi (fp32), unmask (u8), xt_out
- * (int64); per pair: n_mask_after (int32), hit_eos (u8).  1 <= bl <= 64.
+ * (int64); per pair: n_mask_after (int32), hit_eos (u8).  1 <= bl <= 64, 1 <= K <= 64.
  * Two launches: a streaming pass per (pair, position), then one wave per pair.
  * ------------------------------------------------------------------------ */
 

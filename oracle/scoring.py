@@ -56,8 +56,12 @@ def score_step(
     gumbel_tok: Optional[torch.Tensor] = None,   # [B, bl, V] fp32 when temperature > 0
     pos_noise: Optional[torch.Tensor] = None,    # [B, bl] fp32 added on masked positions
     active: Optional[torch.Tensor] = None,       # [B] bool; inactive rows keep xt
+    sampled: Optional[torch.Tensor] = None,      # [B, bl] int64: use these tokens instead of the argmax
 ) -> Dict[str, torch.Tensor]:
-    """server/engine.py:532-593 (fp32), returning every intermediate decision."""
+    """server/engine.py:532-593 (fp32), returning every intermediate decision.
+
+    ``sampled`` replaces the token choice, so the decisions that follow a
+    given (e.g. tied) choice can be recomputed."""
     B, bl, V = logits_c.shape
     lc = logits_c.float()
     lu = None if logits_u is None else logits_u.float()
@@ -72,7 +76,9 @@ def score_step(
         probs_c = lc.softmax(-1)
         probs_u = None
 
-    if temperature > 0:
+    if sampled is not None:
+        sampled = sampled.long()
+    elif temperature > 0:
         assert gumbel_tok is not None
         sampled = (guided / temperature + gumbel_tok).argmax(-1)
     else:

@@ -33,6 +33,7 @@ struct ScoreParams {
   const float* q_tab;
   int K;
   float cfg_w, cfg_w1;  // w and (float)(1 + w)
+  float rank_c;         // (float)((1 + w) / w): argmax rank c*lc - lu (w > 0, no sampling)
   int quantile_on;
   int64_t mask_id, stop_id;
   float temperature;
@@ -104,7 +105,7 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 // kept to the minimum the math needs (bf16 unpack, max, one FMA + v_exp and an
 // add per branch, the guided score and a compare/select for the argmax):
 // with 268 MB of logits this kernel sits at the VALU/HBM balance point.
-template <bool kHasU, bool kSample>
+template <bool kHasU, bool kSample, bool kRank = false>
 __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams P) {
   const int item = blockIdx.x;
   const int pair = item / P.bl;
@@ -126,8 +127,12 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
   float best_g = -INFINITY;
   int best_v = 0x7fffffff;
 
-  // Guided score of element v (+ T * Gumbel noise when sampling).
+  // Guided score of element v (+ T * Gumbel noise when sampling).  Without
+  // sampling only its order matters, and for w > 0 the argmax ranks by
+  // c*lc - lu, c = (1+w)/w: the same order as (1+w)*lc - w*lu (one FMA per
+  // element; exact for bf16 logits at w = 0.5, where c = 3).
   auto guided = [&](float lc, float lu, int v) {
+    if constexpr (kRank) return __builtin_fmaf(P.rank_c, lc, -lu);
     // one rounding less than (1+w)*lc - w*lu; only ulp-level near-ties can tell
     float g = kHasU ? __builtin_fmaf(w1, lc, -w * lu) : lc;
     if (kSample) {
@@ -175,17 +180,19 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
     }
     sc = merge_stats(sc, RowStats{mc, ac});
     if (kHasU) su = merge_stats(su, RowStats{mu, au});
-    // argmax; the first maximum in index order wins, as torch.argmax does.
-    float pg = -INFINITY;
+    // argmax; the first maximum in index order wins, as torch.argmax does:
+    // the maximum by a max3 tree, then the lowest element equal to it (the
+    // guided values reuse the registers of fc, which are dead by now).
+    float gv[2 * kUnroll];
+#pragma unroll
+    for (int e = 0; e < 2 * kUnroll; ++e)
+      gv[e] = guided(fc[e], kHasU ? fu[e] : 0.f, 2 * (base + (e >> 1) * kThreads + tid) + (e & 1));
+    float pg = gv[0];
+#pragma unroll
+    for (int e = 1; e < 2 * kUnroll; ++e) pg = fmaxf(pg, gv[e]);
     int pe = 0;
 #pragma unroll
-    for (int e = 0; e < 2 * kUnroll; ++e) {
-      const float g = guided(fc[e], kHasU ? fu[e] : 0.f, 2 * (base + (e >> 1) * kThreads + tid) + (e & 1));
-      if (g > pg) {
-        pg = g;
-        pe = e;
-      }
-    }
+    for (int e = 2 * kUnroll - 1; e >= 0; --e) pe = gv[e] == pg ? e : pe;
     if (pg > best_g) {
       best_g = pg;
       best_v = 2 * (base + (pe >> 1) * kThreads + tid) + (pe & 1);
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
       const Best o{s_f[q][4], s_i[q], 0.f, 0.f};
       if (better(o, best)) best = o;
     }
-    const int x = best.idx;
+    const int x = best.idx < V ? best.idx : 0;  // a row of only -inf / NaN scores: token 0, as torch.argmax
     const float lpr = P.log_prior[x];
     // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
     const float lcx = bf16_to_f32(rc[x]);
@@ -278,6 +285,12 @@ __global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParam
   const int lane = threadIdx.x & 63;
   const int64_t ib = static_cast<int64_t>(pair) * bl;
   const bool valid = lane < bl;
+  // Every load is independent of every other: the step tables come in
+  // lane-parallel (entry `lane`) and are picked by readlane once k is known.
+  const int64_t k = P.k_step[pair];
+  const float q_lane = lane < P.K ? P.q_tab[lane] : 0.f;
+  const int sched_lane = lane < P.K ? P.sched[lane] : 0;
+  const bool act = P.active == nullptr || P.active[pair] != 0;
   const int64_t xt = valid ? P.xt_in[ib + lane] : 0;
   const float key = valid ? P.pmi[ib + lane] : 0.f;
   const int64_t smp = valid ? P.sampled[ib + lane] : 0;
@@ -293,11 +306,10 @@ __global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParam
       desc += (pj > key) || (pj == key && j < lane);
     }
   }
-  const int64_t k = P.k_step[pair];
   int kc = k < P.K - 1 ? static_cast<int>(k) : P.K - 1;
   kc = kc < 0 ? 0 : kc;
   // p = q_t[k] * (m-1).clamp_min(0).float(); lo/hi = floor/ceil; linear interpolation.
-  const float p = __fmul_rn(P.q_tab[kc], static_cast<float>(m > 1 ? m - 1 : 0));
+  const float p = __fmul_rn(readlane_f(q_lane, kc), static_cast<float>(m > 1 ? m - 1 : 0));
   int lo = static_cast<int>(floorf(p));
   int hi = static_cast<int>(ceilf(p));
   lo = lo < 0 ? 0 : lo;
@@ -308,11 +320,10 @@ __global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParam
   const float v_hi = bhi ? readlane_f(key, __ffsll(static_cast<unsigned long long>(bhi)) - 1) : INFINITY;
   const float tau = __fadd_rn(v_lo, __fmul_rn(__fsub_rn(p, static_cast<float>(lo)), __fsub_rn(v_hi, v_lo)));
   const int n_quant = P.quantile_on ? __popcll(__ballot(msk && key >= tau)) : 0;
-  const int n_sched = min(P.sched[kc], m);
+  const int n_sched = min(__builtin_amdgcn_readlane(sched_lane, kc), m);
   int n = min(max(n_sched, n_quant), m);
   if (k >= P.K - 1) n = m;
   if (m == 0) n = 0;
-  const bool act = P.active == nullptr || P.active[pair] != 0;
   const bool unm = act && msk && desc < n;
   const int64_t xo = unm ? smp : xt;
   if (valid) {
@@ -347,7 +358,7 @@ extern "C" int yapd_score_cfg_pmi_unmask(
                static_cast<long long>(seq_stride), static_cast<long long>(pos_stride));
   YAPD_REQUIRE(pos_stride >= vocab, "score: pos_stride %lld < vocab %d", static_cast<long long>(pos_stride), vocab);
   YAPD_REQUIRE(cond_row0 >= 0 && pair_row_step >= 0, "score: negative row layout");
-  YAPD_REQUIRE(K >= 1, "score: K must be >= 1");
+  YAPD_REQUIRE(K >= 1 && K <= 64, "score: need 1 <= K <= 64 (got %d)", K);
   YAPD_REQUIRE(temperature >= 0.f, "score: temperature must be >= 0");
   YAPD_REQUIRE(log_prior && xt_in && k_step && sched && q_tab, "score: NULL input pointer");
   YAPD_REQUIRE(sampled_out && pmi_out && unmask_out && xt_out && n_mask_after_out && hit_eos_out,
@@ -372,6 +383,7 @@ extern "C" int yapd_score_cfg_pmi_unmask(
   P.K = K;
   P.cfg_w = cfg_w;
   P.cfg_w1 = static_cast<float>(1.0 + static_cast<double>(cfg_w));
+  P.rank_c = cfg_w > 0.f ? static_cast<float>((1.0 + static_cast<double>(cfg_w)) / static_cast<double>(cfg_w)) : 0.f;
   P.quantile_on = quantile_on;
   P.mask_id = mask_id;
   P.stop_id = stop_id;
@@ -389,6 +401,8 @@ extern "C" int yapd_score_cfg_pmi_unmask(
   const dim3 grid(n_pairs * bl), block(yapd::kThreads);
   if (has_uncond && temperature > 0.f)
     hipLaunchKernelGGL((yapd::score_items_kernel<true, true>), grid, block, 0, st, P);
+  else if (has_uncond && cfg_w > 0.f)
+    hipLaunchKernelGGL((yapd::score_items_kernel<true, false, true>), grid, block, 0, st, P);
   else if (has_uncond)
     hipLaunchKernelGGL((yapd::score_items_kernel<true, false>), grid, block, 0, st, P);
   else if (temperature > 0.f)
