@@ -24,4 +24,6 @@ Modules (each function cites the reference file:line it restates):
   calls ``mlx.nn.quantize``; the documented MLX formula is restated).
 * :mod:`oracle.serve` -- the continuous-batching tick bookkeeping of
   server/engine.py:522-620 (commit / denoise transitions, clamps, flags).
+* :mod:`oracle.vocoder` -- the HiFT vocoder's Snake / bias / residual /
+  mean3 elementwise family of server/kernels.py:35-67.
 """

@@ -24,7 +24,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libyapd_t3.so"
 c_int, c_i64, c_u64, c_float, c_size, c_void = (
     ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p)
 
-# name -> (restype, argtypes); mirrors include/yapd_t3.h.
+# name -> (restype, argtypes); mirrors include/yapd_t3.h, yapd_probe.h and yapd_vocoder.h.
 _SIGNATURES = {
     "yapd_last_error": (ctypes.c_char_p, []),
     "yapd_abi_version": (c_int, []),
@@ -55,6 +55,14 @@ _SIGNATURES = {
                                  c_void, c_void]),
     "yapd_t3_block_forward": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void, c_int, c_void,
                                       c_void, c_int, c_void, c_void, c_i64, c_void]),
+    # include/yapd_vocoder.h
+    "yapd_snake": (c_int, [c_void, c_void, c_void, c_void, c_i64, c_int, c_i64, c_void]),
+    "yapd_residual_bias": (c_int, [c_void, c_void, c_void, c_void, c_i64, c_int, c_i64, c_void]),
+    "yapd_mean3": (c_int, [c_void, c_void, c_void, c_void, c_i64, c_void]),
+    "yapd_residual_bias_snake": (c_int, [c_void, c_void, c_void, c_void, c_void, c_void, c_i64, c_int, c_i64,
+                                         c_void]),
+    "yapd_branch_start": (c_int, [c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_i64,
+                                  c_int, c_i64, c_void]),
 }
 
 
