@@ -23,6 +23,10 @@ a bounded sample of the same step.
 128 slots, block 16, K = 10, temperature 0.6, position temperature 5, CFG 1)
 over a queue of requests and reports committed speech tokens per second.
 
+``--workload vocoder`` times the HiFT vocoder's elementwise family on the
+last-stage tensors of a 48-chunk micro-batch of 80-token chunks
+([48, 64, 19201] fp32) against the HBM roofline.
+
 ``--workload attn_stress`` instead measures 30 layers of block attention
 back to back over 256 sequences with log-uniform [64, 2048] prefixes, block
 16, each layer's pages drawn at random from its own 65,536-page pool; and
@@ -59,7 +63,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["step", "attn_stress", "quant", "serve"], default="step")
+    ap.add_argument("--workload", choices=["step", "attn_stress", "quant", "serve", "vocoder"], default="step")
     ap.add_argument("--requests", type=int, default=384, help="serve workload: number of requests")
     ap.add_argument("--kernel-sample", action="store_true",
                     help="only run the dominant GEMM (bench shape) and a 1 GiB copy, for rocprofv3 --pmc")
@@ -99,7 +103,7 @@ def main():
     kernels.load_library()
     dev = torch.device("cuda:0")
     Bp, bl, L = args.pairs, args.block, args.layers
-    if args.kernel_sample:
+    if args.kernel_sample and args.workload == "step":
         kernel_sample(dev, 2 * Bp * bl)
         return
     if args.workload == "attn_stress":
@@ -110,6 +114,9 @@ def main():
         return
     if args.workload == "serve":
         serve(args, dev)
+        return
+    if args.workload == "vocoder":
+        vocoder_workload(args, dev)
         return
     B = 2 * Bp
     D, H, F, V = 1024, 16, 4096, 8194
@@ -305,6 +312,80 @@ def attn_stress(args, dev):
                    "kv_positions_per_layer": sum(kv_len)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": byts // L}}), flush=True)
+
+
+def vocoder_workload(args, dev):
+    """The HiFT generator's elementwise ops between its convolutions (server/kernels.py:35-67)
+    on the last upsampling stage of a 48-job micro-batch of 80-token chunks: 160 mel frames
+    x 120 = 19,200 samples + 1 from the reflection pad, 64 channels, fp32.  Two input sets
+    alternate so no launch finds its inputs in the 256 MB MALL.  Roofline kernel:
+    residual_bias_snake (the resblock's fused residual add + next Snake, 16 B per element)."""
+    from yapd_amd.vocoder import load_snake_extension
+    ops = load_snake_extension()
+    B, C, T = 48, 64, 19201
+    n = B * C * T
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    sets = [[torch.randn(B, C, T, generator=g, device=dev) for _ in range(3)] for _ in range(2)]
+    alpha = [torch.rand(C, generator=g, device=dev) * 2 + 0.2 for _ in range(3)]
+    bias = torch.randn(C, generator=g, device=dev) * 0.1
+    if args.kernel_sample:  # for rocprofv3 --pmc: the roofline kernel and the copy calibration, x3 each
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize(dev)
+        for i in range(3):
+            ops.residual_bias_snake(*sets[i % 2][:2], bias, alpha[0])
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"kernel_sample": "residual_bias_snake [%d, %d, %d] x3; copy %d bytes x3"
+                                           % (B, C, T, COPY_BYTES)}))
+        return
+    it = [0]
+
+    def pick():
+        it[0] ^= 1
+        return sets[it[0]]
+    cases = {  # name -> (launch, fp32 tensors read + written per element)
+        "snake": (lambda: ops.snake(pick()[0], alpha[0]), 2),
+        "snake_bias": (lambda: ops.snake_bias(pick()[0], alpha[0], bias), 2),
+        "residual_bias": (lambda: ops.residual_bias(*pick()[:2], bias), 3),
+        "residual_bias_snake": (lambda: ops.residual_bias_snake(*pick()[:2], bias, alpha[0]), 4),
+        "branch_start": (lambda: ops.branch_start(*pick()[:2], *alpha), 6),
+        "mean3": (lambda: ops.mean3(*pick()), 4),
+    }
+    res = {}
+    for name, (fn, tensors) in cases.items():
+        ms = time_launches(fn, max(args.steps, 10), dev)
+        res[name] = {"us": round(ms * 1e3, 1), "gbs": round(tensors * 4 * n / (ms * 1e-3) / 1e9, 1)}
+        log(f"{name}: {ms * 1e3:.1f} us, {res[name]['gbs']:.0f} GB/s")
+    dom = res["residual_bias_snake"]
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "vocoder_residual_bias_snake_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import vocoder as OV
+        # the whole workload, repeated until at least 10 s of single-threaded numpy (at most 8 passes)
+        x, r = (t.cpu().numpy() for t in sets[0][:2])
+        b_np, a_np = bias.cpu().numpy(), alpha[0].cpu().numpy()
+        passes, t0 = 0, time.time()
+        while passes < 8 and (passes == 0 or time.time() - t0 < 10.0):
+            OV.residual_bias_snake(x, r, b_np, a_np)
+            passes += 1
+        dt = time.time() - t0
+        cpu = {"value": round(passes * 4 * 4 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"residual_bias_snake on [{B}, {C}, {T}] x {passes} with the numpy oracle (float64 Snake), "
+                         f"one thread, {dt:.1f} s"}
+    print(json.dumps({
+        "metric": "HiFT vocoder elementwise HBM GB/s (residual_bias_snake)", "value": dom["gbs"], "unit": "GB/s",
+        "n_gpus": 1, "ms_per_step": round(dom["us"] / 1e3, 4), "higher_is_better": True, "dtype": "f32",
+        "data": "synthetic (N(0,1) activations, alpha U[0.2, 2.2], bias N(0, 0.01))",
+        "config": {"workload": "HiFT last-stage elementwise ops", "batch": B, "channels": C, "samples": T},
+        "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "bytes_per_launch": 4 * 4 * n, "traffic": traffic},
+        "kernels": res, "cpu_baseline": cpu}), flush=True)
 
 
 def serve(args, dev):

@@ -45,7 +45,7 @@ def assert_snake(got, ref64, alpha):
     assert bool((err <= bound).all()), f"max err {err.max().item():.3e}, worst excess {(err - bound).max().item():.3e}"
 
 
-SHAPES = [(2, 5, 37, 0), (3, 64, 1280, 0), (1, 3, 4100, 0), (2, 4, 1024, 1)]
+SHAPES = [(2, 5, 37, 0), (3, 64, 1280, 0), (1, 3, 4100, 0), (2, 4, 1024, 1), (2, 3, 6401, 0)]
 
 
 @pytest.mark.parametrize("B,C,T,off", SHAPES)

@@ -6,8 +6,9 @@
 // Layout of the work: one workgroup owns kChunk consecutive samples of one
 // (b, c) row, so the per-channel alpha / bias values are wave-uniform scalar
 // loads made once per workgroup (no per-element index division), and every
-// thread moves 16-byte vectors when T is a multiple of 4 (HiFT's T is:
-// 80-token chunks give 1280 / 6400 / 19200 samples per stage).  The loads of
+// thread moves 16-byte vectors over the 16-byte-aligned middle of its range,
+// whatever T is (HiFT's last stage has T = 3 * 6400 + 1 after its reflection
+// pad), with at most three elements one by one at either end.  The loads of
 // a thread's vectors are all issued before any is used.  Each op is HBM-bound
 // (8 to 24 bytes per element against a few dozen VALU operations, sinf
 // included), so the roofline is the bytes of the inputs plus the outputs.
@@ -39,7 +40,7 @@ struct VocParams {
   int C;
   int64_t T;
   int64_t chunks;  // workgroups per row
-  int vec;         // 16-byte path: T % 4 == 0 and every pointer 16-byte aligned
+  int vec;         // 16-byte path: every pointer 16-byte aligned
 };
 
 // Snake with the per-channel constants folded: v + inv * sin(v * a)^2,
@@ -88,22 +89,40 @@ __global__ __launch_bounds__(kVThreads) void voc_kernel(const VocParams p) {
     inv[j] = 1.0f / (a[j] + 1.0e-9f);
   }
   float* outs[4] = {p.o0, p.o1, p.o2, p.o3};
-  const int64_t base = row * p.T;
+  // This workgroup's elements, as flat indices [g0, g1) of the [B, C, T] tensors.
+  const int64_t g0 = row * p.T + t0;
+  const int64_t g1 = row * p.T + (t0 + kChunk < p.T ? t0 + kChunk : p.T);
+  auto one = [&](int64_t g) {
+    float o[4];
+    apply<OP>(p, p.x[g], kR ? p.r[g] : 0.f, b, a, inv, o);
+#pragma unroll
+    for (int k = 0; k < kOut; ++k) outs[k][g] = o[k];
+  };
 
   if (p.vec) {
+    // 16-byte vectors over the aligned middle [v0, v1); at most 3 elements
+    // before and after it go one by one.
+    const int64_t v0 = (g0 + 3) & ~int64_t{3};
+    const int64_t v1 = g1 & ~int64_t{3};
+    if (v0 >= v1) {  // a range with no whole aligned vector
+      for (int64_t g = g0 + threadIdx.x; g < g1; g += kVThreads) one(g);
+      return;
+    }
+    if (threadIdx.x < v0 - g0) one(g0 + threadIdx.x);
+    if (threadIdx.x < g1 - v1) one(v1 + threadIdx.x);
     f32x4_t xv[kVecPer], rv[kVecPer];
-    int64_t t[kVecPer];
+    int64_t gv[kVecPer];
 #pragma unroll
     for (int q = 0; q < kVecPer; ++q) {
-      t[q] = t0 + static_cast<int64_t>(q * kVThreads + threadIdx.x) * 4;
-      if (t[q] < p.T) {  // T % 4 == 0: a vector is all in or all out
-        xv[q] = *reinterpret_cast<const f32x4_t*>(p.x + base + t[q]);
-        if (kR) rv[q] = *reinterpret_cast<const f32x4_t*>(p.r + base + t[q]);
+      gv[q] = v0 + static_cast<int64_t>(q * kVThreads + threadIdx.x) * 4;
+      if (gv[q] < v1) {
+        xv[q] = *reinterpret_cast<const f32x4_t*>(p.x + gv[q]);
+        if (kR) rv[q] = *reinterpret_cast<const f32x4_t*>(p.r + gv[q]);
       }
     }
 #pragma unroll
     for (int q = 0; q < kVecPer; ++q) {
-      if (t[q] >= p.T) continue;
+      if (gv[q] >= v1) continue;
       f32x4_t ov[kOut];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -113,31 +132,30 @@ __global__ __launch_bounds__(kVThreads) void voc_kernel(const VocParams p) {
         for (int k = 0; k < kOut; ++k) ov[k][e] = o[k];
       }
 #pragma unroll
-      for (int k = 0; k < kOut; ++k) *reinterpret_cast<f32x4_t*>(outs[k] + base + t[q]) = ov[k];
+      for (int k = 0; k < kOut; ++k) *reinterpret_cast<f32x4_t*>(outs[k] + gv[q]) = ov[k];
     }
   } else {
 #pragma unroll
     for (int q = 0; q < 4 * kVecPer; ++q) {
-      const int64_t t = t0 + q * kVThreads + threadIdx.x;
-      if (t >= p.T) break;
-      float o[4];
-      apply<OP>(p, p.x[base + t], kR ? p.r[base + t] : 0.f, b, a, inv, o);
-#pragma unroll
-      for (int k = 0; k < kOut; ++k) outs[k][base + t] = o[k];
+      const int64_t g = g0 + q * kVThreads + threadIdx.x;
+      if (g >= g1) break;
+      one(g);
     }
   }
 }
 
-// ((a + b) + c) * (1/3), the reference's operation order, over a flat range.
+// ((a + b) + c) * (1/3), the reference's operation order, over a flat range;
+// with vec, 16-byte vectors up to n & ~3 and the last (n % 4) one by one.
 __global__ __launch_bounds__(kVThreads) void mean3_kernel(const float* a, const float* b, const float* c, float* out,
                                                           int64_t n, int vec) {
   constexpr float kThird = 1.0f / 3.0f;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk;
   if (vec) {
+    const int64_t nv = n & ~int64_t{3};
 #pragma unroll
     for (int q = 0; q < kVecPer; ++q) {
       const int64_t t = t0 + static_cast<int64_t>(q * kVThreads + threadIdx.x) * 4;
-      if (t >= n) continue;  // n % 4 == 0
+      if (t >= nv) continue;
       const f32x4_t va = *reinterpret_cast<const f32x4_t*>(a + t);
       const f32x4_t vb = *reinterpret_cast<const f32x4_t*>(b + t);
       const f32x4_t vc = *reinterpret_cast<const f32x4_t*>(c + t);
@@ -146,6 +164,8 @@ __global__ __launch_bounds__(kVThreads) void mean3_kernel(const float* a, const 
       for (int e = 0; e < 4; ++e) vo[e] = ((va[e] + vb[e]) + vc[e]) * kThird;
       *reinterpret_cast<f32x4_t*>(out + t) = vo;
     }
+    const int64_t t = nv + threadIdx.x;
+    if (t0 + kChunk >= n && t < n) out[t] = ((a[t] + b[t]) + c[t]) * kThird;  // the last workgroup
   } else {
 #pragma unroll
     for (int q = 0; q < 4 * kVecPer; ++q) {
@@ -173,7 +193,7 @@ int launch_voc(VocParams p, int64_t B, hipStream_t st, const char* what) {
   const void* ptrs[] = {p.x, p.r, p.o0, p.o1, p.o2, p.o3};
   bool aligned = true;
   for (const void* q : ptrs) aligned = aligned && al16f(q);
-  p.vec = (p.T % 4 == 0) && aligned;
+  p.vec = aligned;
   const dim3 grid(static_cast<unsigned>(B * p.C * p.chunks)), block(kVThreads);
   hipLaunchKernelGGL((voc_kernel<OP>), grid, block, 0, st, p);
   YAPD_LAUNCH_CHECK(what);
@@ -218,7 +238,7 @@ extern "C" int yapd_mean3(const float* a, const float* b, const float* c, float*
   YAPD_REQUIRE(n >= 1, "mean3: n must be >= 1");
   const int64_t wgs = (n + yapd::kChunk - 1) / yapd::kChunk;
   YAPD_REQUIRE(wgs < (int64_t{1} << 31), "mean3: too many elements");
-  const int vec = (n % 4 == 0) && yapd::al16f(a) && yapd::al16f(b) && yapd::al16f(c) && yapd::al16f(out);
+  const int vec = yapd::al16f(a) && yapd::al16f(b) && yapd::al16f(c) && yapd::al16f(out);
   hipLaunchKernelGGL(yapd::mean3_kernel, dim3(static_cast<unsigned>(wgs)), dim3(yapd::kVThreads), 0,
                      static_cast<hipStream_t>(stream), a, b, c, out, n, vec);
   YAPD_LAUNCH_CHECK("mean3 launch");
