@@ -96,7 +96,8 @@ int yapd_kv_gather(const void* kv_pool, int64_t n_pages, const int32_t* table_ro
 
 /* Host-side planner (CPU only, no GPU call): cuts each row's kv_len keys
  * into work items of whole 32-key chunks so that ~target_items items exist,
- * longest first.  work [n_work][4] = (row, key_begin, key_end, slot; slot -1
+ * none shorter than min_split_keys (>= 32) unless the whole row is, longest
+ * first.  work [n_work][4] = (row, key_begin, key_end, slot; slot -1
  * means the item writes the final output), merge [n_merge][3] = (row,
  * first_slot, n_slots).  Replaces the per-block plan() of
  * engines/flashinfer.py:346-411. */

@@ -199,13 +199,17 @@ def score_cfg_pmi_unmask(
 # (a) paged block attention
 # --------------------------------------------------------------------------- #
 
-def attn_plan(kv_len, target_items: int = 192, min_split_keys: int = 128):
+def attn_plan(kv_len, target_items: int = 192, min_split_keys: int = 1024):
     """Host planner: ``(work [n,4] int32, merge [m,3] int32, n_slots)`` numpy arrays.
 
     Rows are cut into work items of whole 32-key chunks so that about
     ``target_items`` items exist (192 is roughly how many four-head work items
     the MI355X keeps in flight, so only rows longer than the average share are
-    split); items are ordered longest first.
+    split), never into items shorter than ``min_split_keys``; items are ordered
+    longest first.  1024 keys (1 MB of K/V per four-head item) is where the
+    split rows' merges and per-item start-up cost less than the tail they
+    remove: on 256 rows of log-uniform [64, 2048] keys, 1024 runs 125 us per
+    layer against 128 us at 128 keys and 131 us at 1280 keys.
     """
     import numpy as np
     kv = np.ascontiguousarray(np.asarray(kv_len, dtype=np.int32))

@@ -73,7 +73,7 @@ class AttnPlan:
     """Device work list + split-KV workspace for one set of per-row kv lengths."""
 
     def __init__(self, kv_len: Sequence[int], bl: int, n_heads: int, device: torch.device,
-                 target_items: int = 192, min_split_keys: int = 128):
+                 target_items: int = 192, min_split_keys: int = 1024):
         work, merge, n_slots = kernels.attn_plan(kv_len, target_items=target_items, min_split_keys=min_split_keys)
         self.kv_len_host = [int(x) for x in kv_len]
         self.work = torch.from_numpy(work).to(device)
