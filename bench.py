@@ -166,8 +166,9 @@ def main():
     ms_qkv = time_launches(lambda: kernels.gemm_qkv_rope_kv(buf.normed, eng._w[nxt()]["wqkv"], eng._cos, eng._sin,
                                                             buf.pos0, bl, buf.q, eng.kv.pools[layer[0]],
                                                             eng.kv.table), 20, dev)
-    ms_o = time_launches(lambda: kernels.gemm_bf16(buf.attn, eng._w[nxt()]["wo"], buf.delta), 20, dev)
-    ms_down = time_launches(lambda: kernels.gemm_bf16(buf.act, eng._w[nxt()]["wd"], buf.delta), 20, dev)
+    # o_proj / down_proj as the step runs them: with the residual add in the epilogue
+    ms_o = time_launches(lambda: kernels.gemm_bf16_residual(buf.attn, eng._w[nxt()]["wo"], buf.delta), 20, dev)
+    ms_down = time_launches(lambda: kernels.gemm_bf16_residual(buf.act, eng._w[nxt()]["wd"], buf.delta), 20, dev)
     eager_plan = AttnPlan(plan.kv_len.tolist(), bl, H, dev)
     ms_attn = time_launches(lambda: eager_plan.run(buf.q.view(B, bl, H, 64), eng.kv.pools[nxt()], eng.kv.table,
                                                    buf.attn.view(B, bl, H, 64), 0.125), 20, dev)

@@ -1,24 +1,26 @@
-// (b) bf16 MFMA GEMMs of the T3 layer with fused epilogues, plus the
-// (residual-add +) RMSNorm row kernels.
+// (b) bf16 MFMA GEMMs of the T3 layer with fused epilogues, plus the RMSNorm
+// row kernel.
 //
 // C[M, N] = A[M, K] * W[N, K]^T (nn.Linear layout), fp32 accumulation on
-// v_mfma_f32_32x32x16_bf16.  A 256-thread workgroup owns a 128 x 128 tile as
-// 2 x 2 waves of 64 x 64 (2 x 2 MFMA tiles each); K advances in steps of 64
-// through double-buffered LDS (rows padded by 16 bytes so the 16-byte
-// fragment reads of 8 consecutive lanes hit distinct banks); the next K step
-// is fetched into registers while the current one is multiplied.
+// v_mfma_f32_32x32x16_bf16.  Large M: `gemm_dl_kernel`, a 256 x 256 tile of
+// 8 waves (128 x 64 each) whose A and W k-slices go global -> LDS by direct
+// loads into two 64 KB stages.  Small M and the quantised W path:
+// `gemm_kernel`, register-staged 128 x 128 (or 256 x 256) tiles with padded
+// LDS rows.  K advances in steps of 64.
 //
-// Epilogues (once per output element, so their VALU cost is small):
-//   * store   -- plain bf16 store (o_proj / down / speech head);
-//   * qkv     -- NeoX RoPE on q and k from a cos/sin table at each row's
-//                absolute position, q to its buffer, k and v straight into
-//                the paged KV pool (engines/flashinfer.py:998-1035);
-//   * swiglu  -- silu(gate) * up from interleaved gate/up weight rows
-//                (engines/flashinfer.py:433-455).
+// Epilogues (once per output element):
+//   * store    -- plain bf16 store (speech head, small projections);
+//   * residual -- C = bf16(C + bf16(acc)): o_proj / down_proj with the
+//                 decoder layer's residual add (engines/flashinfer.py:1040-1060);
+//   * qkv      -- NeoX RoPE on q and k from a cos/sin table at each row's
+//                 absolute position, q to its buffer, k and v straight into
+//                 the paged KV pool (engines/flashinfer.py:998-1035);
+//   * swiglu   -- silu(gate) * up from interleaved gate/up weight rows
+//                 (engines/flashinfer.py:433-455).
 // The bf16 roundings of the reference's separate ops are reproduced (HF
 // computes q*cos, rotate_half(q)*sin and their sum in bf16; silu(g) and the
-// product in bf16), so the fused results differ from it only through the
-// fp32 accumulation order.
+// product in bf16; the residual add of two bf16 values), so the fused results
+// differ from it only through the fp32 accumulation order.
 //
 // A prologue mode "shift" reads A row (r, j) from hidden row (r, j-1) and
 // row (r, 0) from shift_ctx[r]: the token-shifted speech head
@@ -262,6 +264,10 @@ __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f3
                                                    uint16_t* lds, int m0, int n0, int wm, int wn, int lane, int tid) {
   constexpr int CP = T::BN + 8;  // staging row pitch (bf16)
   static_assert(T::BM * CP <= 2 * (T::BM + T::BN) * T::PITCH, "C tile must fit in the LDS staging area");
+  constexpr int CPR = T::BN / 8;                       // 16-byte chunks per tile row
+  constexpr int ITER = T::BM * CPR / T::THREADS;        // chunks per thread
+  static_assert(ITER * T::THREADS == T::BM * CPR, "tile chunks must split evenly over the threads");
+  const bool vec_ok = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
   const int col = lane & 31;
   const int rgrp = 4 * (lane >> 5);
 #pragma unroll
@@ -274,10 +280,25 @@ __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f3
         const int c = wn * T::WTN + 32 * j + col;
         lds[r * CP + c] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][e]));
       }
+  // With ADD, all of this thread's residual chunks are requested at once
+  // (the accumulators are dead now), so they cost one round trip, which the
+  // barrier waits for; loads placed after stores to the same array would
+  // otherwise run one round trip per chunk.
+  u32x4_t res[ADD ? ITER : 1];
+  if constexpr (ADD) {
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int idx = tid + it * T::THREADS;
+      const int r = idx / CPR, cc = (idx % CPR) * 8;
+      const int m = m0 + r, n = n0 + cc;
+      if (vec_ok && m < p.M && n + 8 <= p.N)
+        res[it] = *reinterpret_cast<const u32x4_t*>(p.C + static_cast<int64_t>(m) * p.ldc + n);
+    }
+  }
   __syncthreads();
-  const bool vec_ok = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
-  constexpr int CPR = T::BN / 8;  // 16-byte chunks per tile row
-  for (int idx = tid; idx < T::BM * CPR; idx += T::THREADS) {
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int idx = tid + it * T::THREADS;
     const int r = idx / CPR, cc = (idx % CPR) * 8;
     const int m = m0 + r, n = n0 + cc;
     if (m >= p.M || n >= p.N) continue;
@@ -286,9 +307,9 @@ __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f3
     if (vec_ok && n + 8 <= p.N) {
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
       if constexpr (ADD) {
-        const u32x4_t r = *reinterpret_cast<const u32x4_t*>(dst);
 #pragma unroll
-        for (int w = 0; w < 4; ++w) v[w] = pack_bf16x2(bf16lo(r[w]) + bf16lo(v[w]), bf16hi(r[w]) + bf16hi(v[w]));
+        for (int w = 0; w < 4; ++w)
+          v[w] = pack_bf16x2(bf16lo(res[it][w]) + bf16lo(v[w]), bf16hi(res[it][w]) + bf16hi(v[w]));
       }
       *reinterpret_cast<u32x4_t*>(dst) = v;
     } else {
