@@ -145,3 +145,50 @@ def test_rmsnorm(dev, with_delta):
     ulp = ref.float().abs() * 2 ** -7 + 1e-6
     assert (diff <= ulp).all()
     assert (diff > 0).float().mean().item() < 0.01  # all but a few match bit for bit
+
+
+@pytest.mark.parametrize("epi", ["store", "residual", "swiglu", "qkv"])
+def test_rows_do_not_depend_on_batch_size(dev, epi):
+    """A row computed in a small call (128 x 128 register-staged kernel) is
+    bit-identical to the same row computed inside a large call (256 x 256
+    direct-load kernel): both issue the same MFMA over K in the same order.
+    Continuous batching relies on it -- a request's tokens must not depend on
+    how many requests share its step."""
+    H, D, bl = 16, 1024, 32
+    big, small = 16384, 96
+    A = rnd(big, D, seed=31).to(dev)
+    if epi in ("store", "residual", "swiglu"):
+        N = 8192 if epi == "swiglu" else 1024
+        W = rnd(N, D, std=0.02, seed=32).to(dev)
+        outs = []
+        for M in (big, small):
+            if epi == "store":
+                C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+                kernels.gemm_bf16(A[:M], W, C)
+            elif epi == "residual":
+                C = rnd(M, N, seed=33).to(dev)
+                kernels.gemm_bf16_residual(A[:M], W, C)
+            else:
+                C = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
+                kernels.gemm_swiglu(A[:M], W, C)
+            outs.append(C[:small].cpu())
+        assert torch.equal(outs[0], outs[1])
+        return
+    Wqkv = rnd(3 * H * 64, D, std=0.02, seed=34).to(dev)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
+    fr = torch.outer(torch.arange(1024).float(), inv)
+    emb = torch.cat([fr, fr], -1)
+    cos_t, sin_t = emb.cos().bfloat16().float().to(dev), emb.sin().bfloat16().float().to(dev)
+    rows_big, rows_small = big // bl, small // bl
+    pos0 = torch.from_numpy(np.random.default_rng(5).integers(0, 700, rows_big).astype(np.int32)).to(dev)
+    n_pages = rows_big * 48
+    table = torch.from_numpy(np.random.default_rng(6).permutation(n_pages).reshape(rows_big, 48).astype(np.int32)).to(dev)
+    res = []
+    for M in (big, small):
+        pool = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
+        q_out = torch.empty(M, H * 64, dtype=torch.bfloat16, device=dev)
+        kernels.gemm_qkv_rope_kv(A[:M], Wqkv, cos_t, sin_t, pos0[: M // bl], bl, q_out, pool, table[: M // bl])
+        pages = table[:rows_small].reshape(-1).long()
+        res.append((q_out[:small].cpu(), pool[pages].cpu()))
+    assert torch.equal(res[0][0], res[1][0])
+    assert torch.equal(res[0][1], res[1][1])
