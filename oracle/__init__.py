@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (``yapd_amd``) imports,
 links or runs anything under ``oracle/``.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-use it, and only as the checker (or as the timed CPU baseline), never as the
-thing measured or shipped.
+use it, and only as the reference that GPU results are compared against (or
+as the timed CPU baseline), never as the thing measured or shipped.
 
 Modules (each function cites the reference file:line it restates):
 
