@@ -91,7 +91,7 @@ def time_launches(fn, reps, dev):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU (data-parallel over pairs) is not "
+        print(json.dumps({"error": "yapd_amd runs the step on one GPU; multi-GPU (data-parallel over pairs) is not "
                                    "part of it", "n_gpus": args.gpus}))
         sys.exit(2)
     from yapd_amd import kernels
