@@ -265,11 +265,7 @@ struct MergeParams {
   uint16_t* out;
 };
 
-// One workgroup per (split row, query); a thread owns 4 head-dim values of one head.
-__global__ __launch_bounds__(256) void attn_merge_kernel(const MergeParams P) {
-  if (P.counts != nullptr && static_cast<int>(blockIdx.x) >= P.counts[1]) return;
-  const int3 mi = make_int3(P.merge[blockIdx.x * 3], P.merge[blockIdx.x * 3 + 1], P.merge[blockIdx.x * 3 + 2]);
-  const int q = blockIdx.y;
+__device__ __forceinline__ void merge_one(const MergeParams& P, int3 mi, int q) {
   for (int t = threadIdx.x; t < P.H * 16; t += blockDim.x) {
     const int h = t >> 4;
     const int d0 = (t & 15) * 4;
@@ -291,6 +287,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const MergeParams P) {
     w2[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
     w2[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
     *reinterpret_cast<u32x2_t*>(P.out + ((static_cast<int64_t>(mi.x) * P.bl + q) * P.H + h) * kHeadDim + d0) = w2;
+  }
+}
+
+// A grid-stride loop over (split row, query) pairs, at most kMergeGrid
+// workgroups: with no live split row (the device count of a graph-replayed
+// plan is often 0) the launch is a handful of empty workgroups rather than
+// one per planned slot.  A thread owns 4 head-dim values of one head.
+constexpr int kMergeGrid = 1024;
+
+__global__ __launch_bounds__(256) void attn_merge_kernel(const MergeParams P, int n_merge) {
+  const int live = P.counts != nullptr ? min(P.counts[1], n_merge) : n_merge;
+  for (int it = blockIdx.x; it < live * P.bl; it += gridDim.x) {
+    const int mrow = it / P.bl, q = it - mrow * P.bl;
+    const int3 mi = make_int3(P.merge[mrow * 3], P.merge[mrow * 3 + 1], P.merge[mrow * 3 + 2]);
+    merge_one(P, mi, q);
   }
 }
 
@@ -459,7 +470,9 @@ extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t
   YAPD_LAUNCH_CHECK("attn_paged_kernel launch");
   if (n_merge > 0) {
     yapd::MergeParams M{merge, counts, part_o, part_ml, bl, n_heads, static_cast<uint16_t*>(out)};
-    hipLaunchKernelGGL(yapd::attn_merge_kernel, dim3(n_merge, bl), dim3(256), 0, st, M);
+    const int64_t pairs = static_cast<int64_t>(n_merge) * bl;
+    const dim3 mgrid(static_cast<unsigned>(pairs < yapd::kMergeGrid ? pairs : yapd::kMergeGrid));
+    hipLaunchKernelGGL(yapd::attn_merge_kernel, mgrid, dim3(256), 0, st, M, n_merge);
     YAPD_LAUNCH_CHECK("attn_merge_kernel launch");
   }
   return YAPD_OK;
