@@ -27,6 +27,9 @@ over a queue of requests and reports committed speech tokens per second.
 last-stage tensors of a 48-chunk micro-batch of 80-token chunks
 ([48, 64, 19201] fp32) against the HBM roofline.
 
+``--workload prefill`` times the prefix prefill of the step's rows (causal,
+64-token chunks through the paged KV) in prefix tokens per second.
+
 ``--workload attn_stress`` instead measures 30 layers of block attention
 back to back over 256 sequences with log-uniform [64, 2048] prefixes, block
 16, each layer's pages drawn at random from its own 65,536-page pool; and
@@ -63,7 +66,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["step", "attn_stress", "quant", "serve", "vocoder"], default="step")
+    ap.add_argument("--workload", choices=["step", "attn_stress", "quant", "serve", "vocoder", "prefill"],
+                    default="step")
     ap.add_argument("--requests", type=int, default=384, help="serve workload: number of requests")
     ap.add_argument("--kernel-sample", action="store_true",
                     help="only run the dominant GEMM (bench shape) and a 1 GiB copy, for rocprofv3 --pmc")
@@ -117,6 +121,9 @@ def main():
         return
     if args.workload == "vocoder":
         vocoder_workload(args, dev)
+        return
+    if args.workload == "prefill":
+        prefill_workload(args, dev)
         return
     B = 2 * Bp
     D, H, F, V = 1024, 16, 4096, 8194
@@ -313,6 +320,67 @@ def attn_stress(args, dev):
                    "kv_positions_per_layer": sum(kv_len)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": byts // L}}), flush=True)
+
+
+def prefill_workload(args, dev):
+    """Prefix prefill (HipEngine.prefix_forward, engines/flashinfer.py:678-854 semantics) of the
+    step's 512 rows: prefixes U[150, 600] per pair (cond and null rows share the length), 30
+    layers, causal 64-token chunks writing the paged KV.  Algorithmic work: the projections of
+    the real prefix tokens (2 * D * 16,384 flops per token and layer) plus causal attention;
+    padding the engine computes would count against the rate."""
+    from yapd_amd.engines.hip import HipEngine
+    from yapd_amd.synthetic import make_t3, uniform_lengths
+    Bp, L, D = args.pairs, args.layers, 1024
+    model = make_t3(n_layers=L, seed=args.seed, device=dev)
+    lens = uniform_lengths(Bp, 150, 600, seed=args.seed + 1)
+    lps = lens + lens
+    eng = HipEngine(model, max(lps) + 64, torch.bfloat16, batch_size=len(lps), page_table_seed=args.seed + 2)
+    g = torch.Generator().manual_seed(args.seed + 3)
+    embs = [torch.randn(lp, D, generator=g).to(torch.bfloat16).to(dev) for lp in lps]
+    eng.prefix_forward(embs)  # warm-up (plans, buffers)
+    torch.cuda.synchronize(dev)
+    reps = max(2, args.steps // 5)
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.time()
+    st.record()
+    for _ in range(reps):
+        eng.prefix_forward(embs)
+    en.record()
+    torch.cuda.synchronize(dev)
+    wall = (time.time() - t0) / reps
+    ms = st.elapsed_time(en) / reps
+    tokens = sum(lps)
+    flops = 2.0 * tokens * D * 16384 * L + sum(4.0 * 16 * 64 * lp * (lp + 1) / 2 for lp in lps) * L
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"prefill: {len(lps)} rows, {tokens} prefix tokens, {ms:.1f} ms ({wall * 1e3:.1f} ms wall), "
+        f"{tokens / (ms * 1e-3):.0f} tokens/s, {tflops:.0f} TF/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from dataclasses import replace
+        from oracle import llama as OL
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        n_rows, n_layers = 8, 2
+        bb = OL.backbone_from_model(model, max_pos=max(lps) + 64, dtype=torch.bfloat16)
+        bb = replace(bb, layers=bb.layers[:n_layers])
+        cache = OL.KVCache.empty(n_layers, n_rows, max(lps), 16, 64, torch.bfloat16)
+        sample = [e.cpu() for e in embs[:n_rows]]
+        t = time.time()
+        OL.prefix_forward(bb, sample, cache)
+        dt = (time.time() - t) * L / n_layers
+        cpu = {"value": round(sum(lps[:n_rows]) / dt, 1), "unit": "prefix tokens/s", "cores": threads, "kind": "port",
+               "sample": f"oracle torch-CPU bf16 causal prefill of {n_rows} rows ({sum(lps[:n_rows])} tokens), "
+                         f"{n_layers} of {L} layers, time x {L}/{n_layers}"}
+    print(json.dumps({
+        "metric": "prefix prefill tokens/sec, 30-layer T3, 512 rows", "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "prefix tokens/s", "n_gpus": 1, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic (seeded random-init T3 weights, N(0,1) prefix embeddings)",
+        "config": {"workload": "prefix prefill (causal 64-token chunks, paged KV)", "rows": len(lps),
+                   "prefix_len": "U[150,600] per pair", "layers": L, "prefix_tokens": tokens,
+                   "wall_ms": round(wall * 1e3, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_prefill": flops, "traffic": None},
+        "cpu_baseline": cpu}), flush=True)
 
 
 def vocoder_workload(args, dev):

@@ -239,20 +239,25 @@ class HipEngine:
             kernels.ptr(getattr(plan, "counts", None)), kernels.ptr(plan.part_o), kernels.ptr(plan.part_ml),
             int(plan.n_slots))
 
-    def _descriptor(self, row0: int) -> "kernels.T3Model":
-        """The native model descriptor whose batch row 0 is page-table row ``row0``."""
-        if row0 == 0:
+    def _descriptor(self, row0: int, table: Optional[Tensor] = None) -> "kernels.T3Model":
+        """The native model descriptor whose batch row 0 is page-table row ``row0``, or whose
+        rows are those of ``table`` (page-table rows gathered for a subset of the batch)."""
+        if table is None and row0 == 0:
             return self._c_model
         m = kernels.T3Model.from_buffer_copy(self._c_model)
-        m.page_table = self._kv.table.data_ptr() + row0 * self._kv.table.stride(0) * self._kv.table.element_size()
+        if table is not None:
+            m.page_table = table.data_ptr()
+            m.table_stride = table.stride(0)
+        else:
+            m.page_table = self._kv.table.data_ptr() + row0 * self._kv.table.stride(0) * self._kv.table.element_size()
         return m
 
     def _run(self, buf: _Buffers, plan, kv_len_dev: Tensor, *, causal: bool = False,
              head_w: Optional[Tensor] = None, shift_ctx: Optional[Tensor] = None,
-             logits: Optional[Tensor] = None, row0: int = 0) -> None:
+             logits: Optional[Tensor] = None, row0: int = 0, table: Optional[Tensor] = None) -> None:
         ws = self._workspace(buf, plan)
         V = 0 if head_w is None else int(head_w.shape[0])
-        c_model = self._descriptor(row0)
+        c_model = self._descriptor(row0, table)
         kernels.check(kernels.load_library().yapd_t3_block_forward(
             ctypes.byref(c_model), ctypes.byref(ws), buf.emb.data_ptr(), buf.rows, buf.bl,
             buf.pos0.data_ptr(), kv_len_dev.data_ptr(), int(causal), buf.hidden.data_ptr(),
@@ -297,31 +302,38 @@ class HipEngine:
         return sos
 
     def _prefill(self, row0: int, embs: List[Tensor]) -> Tensor:
-        """Causal forward of ragged prefixes in 64-token chunks on batch rows row0..; pad tokens
-        only write KV past each row's prefix (overwritten by later blocks, never attended)."""
+        """Causal forward of ragged prefixes in 64-token chunks on batch rows row0..  A chunk
+        runs only the rows whose prefix reaches into it (through a page table gathered for
+        them when they are not all the rows), so ragged batches compute no chunk of padding;
+        a row's last chunk is padded, and its pad tokens only write KV past the prefix
+        (overwritten by later blocks, never attended)."""
         n, D = len(embs), self._hidden
         lps = [int(e.shape[0]) for e in embs]
         if min(lps) < 1 or max(lps) > self._max_seq_len:
             raise ValueError("prefix length must be in [1, max_seq_len]")
         lp_max = max(lps)
-        sos = torch.empty(n, 1, D, dtype=self._dtype, device=self._device)
-        done = [False] * n
+        dev, dt = self._device, self._dtype
+        padded = torch.nn.utils.rnn.pad_sequence([e.to(device=dev, dtype=dt) for e in embs], batch_first=True)
+        sos = torch.empty(n, 1, D, dtype=dt, device=dev)
         for c0 in range(0, lp_max, PREFILL_CHUNK):
             bl = min(PREFILL_CHUNK, lp_max - c0)
-            buf = self._buffers(n, bl)
-            buf.emb.zero_()
-            for r, e in enumerate(embs):
-                k = max(0, min(bl, lps[r] - c0))
-                if k > 0:
-                    buf.emb[r * bl: r * bl + k].copy_(e[c0: c0 + k].to(self._dtype))
+            active = [r for r in range(n) if lps[r] > c0]
+            na = len(active)
+            buf = self._buffers(na, bl)
+            table = None
+            if na == n:
+                buf.emb.view(n, bl, D).copy_(padded[:, c0: c0 + bl])
+            else:
+                idx = torch.tensor(active, dtype=torch.long, device=dev)
+                buf.emb.view(na, bl, D).copy_(padded[idx, c0: c0 + bl])
+                table = self._kv.table[idx + row0]
             buf.pos0.fill_(c0)
-            plan = self._plan([c0 + bl] * n, bl)
-            self._run(buf, plan, plan.kv_len, causal=True, row0=row0)
-            hid = buf.hidden.view(n, bl, D)
-            for r in range(n):
-                if not done[r] and c0 <= lps[r] - 1 < c0 + bl:
-                    sos[r, 0] = hid[r, lps[r] - 1 - c0]
-                    done[r] = True
+            plan = self._plan([c0 + bl] * na, bl)
+            self._run(buf, plan, plan.kv_len, causal=True, row0=row0, table=table)
+            last = [(i, r) for i, r in enumerate(active) if c0 <= lps[r] - 1 < c0 + bl]
+            if last:
+                hid = buf.hidden.view(na, bl, D)
+                sos[[r for _, r in last], 0] = hid[[i for i, _ in last], [lps[r] - 1 - c0 for _, r in last]]
         return sos
 
     # ------------------------------------------------------------------ #
