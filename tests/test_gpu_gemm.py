@@ -149,19 +149,21 @@ def test_rmsnorm(dev, with_delta):
 
 @pytest.mark.parametrize("epi", ["store", "residual", "swiglu", "qkv"])
 def test_rows_do_not_depend_on_batch_size(dev, epi):
-    """A row computed in a small call (128 x 128 register-staged kernel) is
-    bit-identical to the same row computed inside a large call (256 x 256
-    direct-load kernel): both issue the same MFMA over K in the same order.
-    Continuous batching relies on it -- a request's tokens must not depend on
-    how many requests share its step."""
+    """A row is bit-identical whether it is computed in a large call (256 x 256
+    direct-load kernel), a mid-sized one (128 x 128 register-staged kernel) or
+    a small one (one-wave 64 x 64 direct-load kernel): all issue the same MFMA
+    over K in the same order.  Continuous batching relies on it -- a request's
+    tokens must not depend on how many requests share its step.  The mid size
+    per epilogue is one that selects the 128 x 128 kernel."""
     H, D, bl = 16, 1024, 32
     big, small = 16384, 96
+    mid = {"store": 4096, "residual": 4096, "swiglu": 1024, "qkv": 2048}[epi]
     A = rnd(big, D, seed=31).to(dev)
     if epi in ("store", "residual", "swiglu"):
         N = 8192 if epi == "swiglu" else 1024
         W = rnd(N, D, std=0.02, seed=32).to(dev)
         outs = []
-        for M in (big, small):
+        for M in (big, mid, small):
             if epi == "store":
                 C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
                 kernels.gemm_bf16(A[:M], W, C)
@@ -173,6 +175,7 @@ def test_rows_do_not_depend_on_batch_size(dev, epi):
                 kernels.gemm_swiglu(A[:M], W, C)
             outs.append(C[:small].cpu())
         assert torch.equal(outs[0], outs[1])
+        assert torch.equal(outs[0], outs[2])
         return
     Wqkv = rnd(3 * H * 64, D, std=0.02, seed=34).to(dev)
     inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
@@ -184,11 +187,12 @@ def test_rows_do_not_depend_on_batch_size(dev, epi):
     n_pages = rows_big * 48
     table = torch.from_numpy(np.random.default_rng(6).permutation(n_pages).reshape(rows_big, 48).astype(np.int32)).to(dev)
     res = []
-    for M in (big, small):
+    for M in (big, mid, small):
         pool = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
         q_out = torch.empty(M, H * 64, dtype=torch.bfloat16, device=dev)
         kernels.gemm_qkv_rope_kv(A[:M], Wqkv, cos_t, sin_t, pos0[: M // bl], bl, q_out, pool, table[: M // bl])
         pages = table[:rows_small].reshape(-1).long()
         res.append((q_out[:small].cpu(), pool[pages].cpu()))
-    assert torch.equal(res[0][0], res[1][0])
-    assert torch.equal(res[0][1], res[1][1])
+    for r in res[1:]:
+        assert torch.equal(res[0][0], r[0])
+        assert torch.equal(res[0][1], r[1])

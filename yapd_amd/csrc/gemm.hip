@@ -4,9 +4,11 @@
 // C[M, N] = A[M, K] * W[N, K]^T (nn.Linear layout), fp32 accumulation on
 // v_mfma_f32_32x32x16_bf16.  Large M: `gemm_dl_kernel`, a 256 x 256 tile of
 // 8 waves (128 x 64 each) whose A and W k-slices go global -> LDS by direct
-// loads into two 64 KB stages.  Small M and the quantised W path:
-// `gemm_kernel`, register-staged 128 x 128 (or 256 x 256) tiles with padded
-// LDS rows.  K advances in steps of 64.
+// loads into two 64 KB stages.  Small M: the same kernel on one-wave 64 x 64
+// tiles with three stages.  Mid M and the quantised W path: `gemm_kernel`,
+// register-staged 128 x 128 (or 256 x 256) tiles with padded LDS rows.  Every
+// kernel runs the same MFMA over the same K order, so a row's result does not
+// depend on which kernel the batch size selects.  K advances in steps of 64.
 //
 // Epilogues (once per output element):
 //   * store    -- plain bf16 store (speech head, small projections);
@@ -557,19 +559,30 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
 // bank groups (two 128-byte rows share one 256-byte bank line).  A load
 // instruction covers 8 rows; lane i writes slot i % 8 of row i / 8, so it
 // fetches the chunk that belongs there.
-template <class T>
+template <class T, int NS>
 struct DlLayout {
   static_assert(T::BK == 64, "direct-load tiles use 128-byte LDS rows");
   static constexpr int WAVES = T::THREADS / 64;
+  static_assert(NS == 2 || (WAVES == 1 && NS >= 2 && NS <= 4), "more than two stages need a one-wave tile");
   static constexpr int ROWB = 128;
   static constexpr int A_BYTES = T::BM * ROWB, B_BYTES = T::BN * ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int LA = T::BM / 8 / WAVES;  // 1 KB loads per wave and k-tile
   static constexpr int LB = T::BN / 8 / WAVES;
   static_assert(LA * 8 * WAVES == T::BM && LB * 8 * WAVES == T::BN, "rows must split evenly over the waves");
+  static constexpr int LPT = LA + LB;  // loads per wave and k-tile
+  static_assert((NS - 2) * LPT <= 63, "the vmcnt counter holds at most 63 loads");
   static constexpr int C_BYTES = T::BM * (T::BN + 8) * 2;  // store-epilogue staging
-  static constexpr int LDS = 2 * STAGE > C_BYTES ? 2 * STAGE : C_BYTES;
+  static constexpr int LDS = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
 };
+
+// Wait until at most N of this wave's vector-memory loads are outstanding
+// (they complete in issue order).  The memory clobber keeps the LDS reads
+// that follow below the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // 16 bytes per lane from src into LDS at lds_run + 16 * lane (lds_run must be
 // the same for the whole wave: it is the M0 base of global_load_lds_dwordx4).
@@ -578,9 +591,9 @@ __device__ __forceinline__ void load_lds16(const uint16_t* src, char* lds_run) {
       src, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(lds_run)), 16, 0, 0);
 }
 
-template <class T, int EPI, int AM>
+template <class T, int EPI, int AM, int NS>
 __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p) {
-  using L = DlLayout<T>;
+  using L = DlLayout<T, NS>;
   // Dynamic LDS: the compiler cannot see the DMA writes into a static
   // __shared__ array and would treat its contents as undefined.
   extern __shared__ __attribute__((aligned(16))) uint16_t dyn_lds[];
@@ -669,29 +682,54 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
     __builtin_amdgcn_sched_group_barrier(0x008, T::TM * T::TN - (T::TM + T::TN), 0);
   };
 
-  // Two LDS stages.  Tile kt+1 is requested at the top of tile kt (its stage
-  // was last read in tile kt-1, before the barrier that ended it); the
-  // barrier at the end of tile kt waits for this wave's loads (the fence of
-  // __syncthreads drains vmcnt) and for every wave's.
+  // NS LDS stages, NS - 1 tiles in flight.  Tile kt+NS-1 is requested at the
+  // top of tile kt into the stage tile kt-1 used: its last fragments were
+  // consumed by the MFMAs that ended tile kt-1.  Before the first fragments
+  // of tile kt+1 are read, the wave waits for its loads of that tile.  With
+  // several waves the barrier (whose fence drains vmcnt) also covers the
+  // other waves' loads; a one-wave tile waits on its own vmcnt and keeps the
+  // later tiles in flight.
   const int kt_n = p.K / T::BK;
-  issue(0, 0);
+#pragma unroll
+  for (int s = 0; s + 1 < NS; ++s)
+    if (s < kt_n) issue(s, s);
   const RowMeta rm = EPI == kEpiQkv ? qkv_row_meta<T>(p, m0, tid) : RowMeta{0, 0};
-  __syncthreads();
+  // Tiles issued after tile t, when the fragments of tile t are first read.
+  auto wait_tile = [&](int t) {
+    if constexpr (L::WAVES > 1) {
+      __syncthreads();
+    } else if constexpr (NS == 2) {
+      wait_vmcnt<0>();
+    } else {
+      if (min(t + NS - 2, kt_n - 1) - t == NS - 2) {
+        wait_vmcnt<(NS - 2) * L::LPT>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    }
+  };
+  wait_tile(0);
   read_frags(0, 0, 0);
+  int stage = 0;
   for (int kt = 0; kt < kt_n; ++kt) {
-    const int buf = kt & 1;
     const bool more = kt + 1 < kt_n;
-    if (more) issue(kt + 1, buf ^ 1);
+    const int next = stage + 1 == NS ? 0 : stage + 1;
+    if (kt + NS - 1 < kt_n) issue(kt + NS - 1, stage == 0 ? NS - 1 : stage - 1);
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
-      read_frags(buf, ks + 1, (ks + 1) & 1);
+      read_frags(stage, ks + 1, (ks + 1) & 1);
       mfma_step(ks & 1);
       interleave();
     }
-    __syncthreads();
-    if (more) read_frags(buf ^ 1, 0, 0);
+    if (more) {
+      wait_tile(kt + 1);
+      read_frags(next, 0, 0);
+    } else if constexpr (L::WAVES > 1) {
+      __syncthreads();  // every wave is done with the stages before the epilogue reuses LDS
+    }
     mfma_step((KS - 1) & 1);
     if (more) interleave();
+    stage = next;
   }
   finish_tile<T, EPI>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
 }
@@ -774,24 +812,25 @@ int launch_tile(const GemmParams& p, hipStream_t st) {
   return YAPD_OK;
 }
 
-template <class T, int EPI, int AM>
+template <class T, int EPI, int AM, int NS = 2>
 int launch_dl(const GemmParams& p, hipStream_t st) {
-  using L = DlLayout<T>;
+  using L = DlLayout<T, NS>;
   static bool lds_set = false;  // the attribute is per kernel; setting it twice is harmless
   if (!lds_set) {
-    if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dl_kernel<T, EPI, AM>),
+    if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dl_kernel<T, EPI, AM, NS>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS),
                            "gemm_dl_kernel LDS attribute"))
       return rc;
     lds_set = true;
   }
   const dim3 grid((p.N + T::BN - 1) / T::BN, (p.M + T::BM - 1) / T::BM), block(T::THREADS);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, EPI, AM>), grid, block, L::LDS, st, p);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, EPI, AM, NS>), grid, block, L::LDS, st, p);
   YAPD_LAUNCH_CHECK("gemm_dl_kernel launch");
   return YAPD_OK;
 }
 
 using TileD = Tile<256, 256, BK, 2, 4>;  // direct-load large tile
+using TileW = Tile<64, 64, BK, 1, 1>;     // direct-load one-wave tile (small batches)
 
 // Compute units of the current device (cached per device id).
 int cu_count() {
@@ -817,6 +856,17 @@ int launch_gemm(GemmParams p, hipStream_t st) {
     p.xcd_band = big_tiles <= cu_count() ? 1 : 0;
     if constexpr (BQ == 0) return launch_dl<TileD, EPI, AM>(p, st);
     return launch_tile<TileL, EPI, AM, BQ>(p, st);
+  }
+  // Few tiles (small batches): one-wave 64 x 64 direct-load tiles with two
+  // k-tiles in flight, while they give at most two workgroups per CU
+  // (measured down at M = 256..2048: 46-51 -> 36-41 us; beyond that the
+  // 128 x 128 kernel is faster).
+  if constexpr (BQ == 0) {
+    const int64_t wave_tiles = static_cast<int64_t>((p.M + 63) / 64) * ((p.N + 63) / 64);
+    if (wave_tiles <= 2 * cu_count()) {
+      p.xcd_band = wave_tiles <= cu_count() ? 1 : 0;
+      return launch_dl<TileW, EPI, AM, 3>(p, st);
+    }
   }
   const int64_t small_tiles = static_cast<int64_t>((p.M + 127) / 128) * ((p.N + 127) / 128);
   p.xcd_band = small_tiles <= cu_count() ? 1 : 0;
