@@ -210,47 +210,55 @@ __device__ __forceinline__ void epilogue_qkv(const GemmParams& p, const f32x16_t
   }
 }
 
-// swiglu epilogue: each 64-column group of W holds the gate rows of 32
-// features, then their up rows, so tile 2q is gate and tile 2q+1 is up of
-// features (n_base + 64q)/2 + col.  silu(g) and the product are rounded to
-// bf16 as the reference's separate ops are; silu uses the hardware
-// reciprocal (<= 1 ulp in fp32 before the bf16 rounding).  The bf16 results
-// are parked in LDS and written as 16-byte row chunks.
+// swiglu epilogue.  Each 64-column group of W holds the gate rows of 32
+// features, then their up rows, so tiles 2q and 2q+1 of a wave are gate and
+// up of the same 32 features.  The swiglu GEMM multiplies W x A^T (MFMA
+// operands swapped, as for qkv): lane l holds token (l & 31) of each 32-row
+// block and features 8 * (e / 4) + 4 * (l / 32) + e % 4 of the group for
+// accumulator element e -- four runs of 4 consecutive features.  silu(g) and
+// the product are rounded to bf16 as the reference's separate ops are; silu
+// uses the hardware reciprocal (<= 1 ulp in fp32 before the bf16 rounding).
+// Neighbouring features share each bf16 conversion, and every run leaves as
+// one 8-byte store straight from registers.
 template <class T>
-__device__ __forceinline__ void epilogue_swiglu(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
-                                                uint16_t* lds, int m0, int n0, int wm, int wn, int lane, int tid) {
-  constexpr int FW = T::BN / 2;  // features per workgroup tile
-  constexpr int CP = FW + 8;     // staging row pitch (bf16)
-  const int col = lane & 31;
-  const int rgrp = 4 * (lane >> 5);
+__device__ __forceinline__ void epilogue_swiglu(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN], int m0,
+                                                int n0, int wm, int wn, int lane) {
+  const int F = p.N / 2;
+  const int tok = lane & 31;
+  const int fsub = 4 * (lane >> 5);
+  const bool vec_ok = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 7u) == 0);
+  auto silu_mul = [](float g0, float g1, float u0, float u1) {
+    const uint32_t gp = pack_bf16x2(g0, g1), up = pack_bf16x2(u0, u1);
+    const float gb0 = bf16lo(gp), gb1 = bf16hi(gp);
+    const uint32_t sp = pack_bf16x2(gb0 * __builtin_amdgcn_rcpf(1.f + __expf(-gb0)),
+                                    gb1 * __builtin_amdgcn_rcpf(1.f + __expf(-gb1)));
+    return pack_bf16x2(bf16lo(sp) * bf16lo(up), bf16hi(sp) * bf16hi(up));
+  };
 #pragma unroll
-  for (int q2 = 0; q2 < T::TN / 2; ++q2) {
-    const int fl = wn * (T::WTN / 2) + 32 * q2 + col;
+  for (int i = 0; i < T::TM; ++i) {
+    const int m = m0 + wm * T::WTM + 32 * i + tok;
+    if (m >= p.M) continue;
+    uint16_t* const row = p.C + static_cast<int64_t>(m) * p.ldc;
 #pragma unroll
-    for (int i = 0; i < T::TM; ++i)
+    for (int q2 = 0; q2 < T::TN / 2; ++q2) {
+      const int fb = (n0 + wn * T::WTN + 64 * q2) / 2;
+      if (fb >= F) continue;  // F % 64 == 0: a group is all in or all out
+      const f32x16_t& g = acc[i][2 * q2];
+      const f32x16_t& u = acc[i][2 * q2 + 1];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int rl = wm * T::WTM + 32 * i + 8 * (e >> 2) + rgrp + (e & 3);
-        const float g = bf16r(acc[i][2 * q2][e]);
-        const float u = bf16r(acc[i][2 * q2 + 1][e]);
-        const float s = bf16r(g * __builtin_amdgcn_rcpf(1.f + __expf(-g)));
-        lds[rl * CP + fl] = static_cast<uint16_t>(f32_to_bf16(s * u));
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int e = 4 * r4;
+        const u32x2_t y = {silu_mul(g[e], g[e + 1], u[e], u[e + 1]), silu_mul(g[e + 2], g[e + 3], u[e + 2], u[e + 3])};
+        uint16_t* dst = row + fb + 8 * r4 + fsub;
+        if (vec_ok) {
+          *reinterpret_cast<u32x2_t*>(dst) = y;
+        } else {
+          dst[0] = static_cast<uint16_t>(y[0] & 0xffffu);
+          dst[1] = static_cast<uint16_t>(y[0] >> 16);
+          dst[2] = static_cast<uint16_t>(y[1] & 0xffffu);
+          dst[3] = static_cast<uint16_t>(y[1] >> 16);
+        }
       }
-  }
-  __syncthreads();
-  const int F = p.N / 2, f0 = n0 / 2;
-  const bool vec_ok = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
-  constexpr int CPR = FW / 8;
-  for (int idx = tid; idx < T::BM * CPR; idx += T::THREADS) {
-    const int r = idx / CPR, cc = (idx % CPR) * 8;
-    const int m = m0 + r, f = f0 + cc;
-    if (m >= p.M || f >= F) continue;  // F % 64 == 0: a chunk is all in or all out
-    const uint16_t* src = lds + r * CP + cc;
-    uint16_t* dst = p.C + static_cast<int64_t>(m) * p.ldc + f;
-    if (vec_ok) {
-      *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
-    } else {
-      for (int t = 0; t < 8; ++t) dst[t] = src[t];
     }
   }
 }
@@ -366,7 +374,7 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, const f32x16_t 
   } else if constexpr (EPI == kEpiResidual) {
     store_tile_via_lds<T, true>(p, acc, lds, m0, n0, wm, wn, lane, tid);
   } else if constexpr (EPI == kEpiSwiglu) {
-    epilogue_swiglu<T>(p, acc, lds, m0, n0, wm, wn, lane, tid);
+    epilogue_swiglu<T>(p, acc, m0, n0, wm, wn, lane);
   } else {
     RowMeta* meta = reinterpret_cast<RowMeta*>(lds);
     if (tid < T::BM) meta[tid] = rm;
@@ -506,7 +514,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
       for (int j = 0; j < T::TN; ++j)
-        acc[i][j] = EPI == kEpiQkv  // transposed product for the qkv epilogue
+        acc[i][j] = EPI == kEpiQkv || EPI == kEpiSwiglu  // transposed product for these epilogues
                         ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0)
                         : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
   };
@@ -667,7 +675,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
       for (int j = 0; j < T::TN; ++j)
-        acc[i][j] = EPI == kEpiQkv  // transposed product for the qkv epilogue
+        acc[i][j] = EPI == kEpiQkv || EPI == kEpiSwiglu  // transposed product for these epilogues
                         ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0)
                         : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
   };
