@@ -63,9 +63,10 @@ def test_gemm_padded_ldc_and_strided_a(dev):
     assert torch.count_nonzero(out_full[:, N:]) == 0  # nothing written past N
 
 
-@pytest.mark.parametrize("M", [300, 2000])  # 2000: large-tile path
-def test_gemm_swiglu(dev, M):
-    K, Fd = 1024, 4096
+@pytest.mark.parametrize("M,K", [(300, 1024), (2000, 1024),  # 2000: large-tile path, one round of tiles
+                                 (4100, 1024), (4100, 256)])  # several rounds (persistent kernel); ragged M; K < 16 k-tiles
+def test_gemm_swiglu(dev, M, K):
+    Fd = 4096
     A = rnd(M, K, seed=5)
     Wg = rnd(Fd, K, std=0.02, seed=6)
     Wu = rnd(Fd, K, std=0.02, seed=7)
