@@ -96,8 +96,6 @@ __device__ __forceinline__ const uint16_t* a_row_ptr(const GemmParams& p, int m)
   return p.A + static_cast<int64_t>(m) * p.lda;
 }
 
-__device__ __forceinline__ float bf16r(float x) { return round_bf16(x); }
-
 // Position and KV page of one tile row for the qkv epilogue.  Computed at
 // kernel start by thread `row` (< BM), so the loads of pos0 and of the page
 // table overlap the main loop; parked in LDS for the epilogue.
@@ -121,20 +119,18 @@ __device__ __forceinline__ RowMeta qkv_row_meta(const GemmParams& p, int m0, int
   return rm;
 }
 
-// qkv epilogue: tiles 2q, 2q+1 of a wave are head dims d and d + 32 of one
-// head of q, k or v (n_base is a multiple of 64 and 64 divides n_heads * 64).
-// NeoX RoPE on q and k from the cos/sin tables at each row's position; the
-// tables are HF's cat(freqs, freqs) layout, so column d + 32 equals column d
-// and only columns 0..31 are read.  `lds` holds the RowMeta of the tile rows.
-// qkv epilogue.  The qkv GEMM multiplies W x A^T (MFMA operands swapped), so
-// lane l holds token (l & 31) of each 32-row block and, in each 32-column
-// block, head dims 8 * (e / 4) + 4 * (l / 32) + e % 4 for accumulator
-// element e: four runs of 4 consecutive dims.  Tiles 2q, 2q+1 of a wave are
-// dims d and d + 32 of one head of q, k or v (the section is uniform per
-// wave: n_base is a multiple of 64 and 64 divides n_heads * 64).  So a lane
-// does RoPE on whole runs (16-byte cos/sin loads), stores q and k as 8-byte
-// runs, and a V column (layout d * 16 + slot) is written by 32 lanes with
-// consecutive slots.  `meta` holds the RowMeta of the tile rows.
+// qkv epilogue: NeoX RoPE on q and k from the cos/sin tables at each row's
+// position; the tables are HF's cat(freqs, freqs) layout, so column d + 32
+// equals column d and only columns 0..31 are read.  The qkv GEMM multiplies
+// W x A^T (MFMA operands swapped), so lane l holds token (l & 31) of each
+// 32-row block and, in each 32-column block, head dims
+// 8 * (e / 4) + 4 * (l / 32) + e % 4 for accumulator element e: four runs of
+// 4 consecutive dims.  Tiles 2q, 2q+1 of a wave are dims d and d + 32 of one
+// head of q, k or v (the section is uniform per wave: n_base is a multiple of
+// 64 and 64 divides n_heads * 64).  So a lane does RoPE on whole runs
+// (16-byte cos/sin loads), stores q and k as 8-byte runs, and a V column
+// (layout d * 16 + slot) is written by 32 lanes with consecutive slots.
+// `meta` holds the RowMeta of the tile rows.
 template <class T, int SECTION>
 __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
                                                      const RowMeta* meta, int m0, int nb, int q2, int wm, int lane) {
@@ -154,26 +150,32 @@ __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const 
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const int d0 = 8 * r4 + dgrp;
-      float x0[4], x1[4];  // dims d0 + t and d0 + 32 + t
+      // Dims d0 + t (x0) and d0 + 32 + t (x1), rounded to bf16 two at a time:
+      // a packed pair holds dims (t, t + 1), which is also the store layout.
+      uint32_t X0[2], X1[2];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        x0[t] = bf16r(acc[i][2 * q2][4 * r4 + t]);
-        x1[t] = bf16r(acc[i][2 * q2 + 1][4 * r4 + t]);
+      for (int h = 0; h < 2; ++h) {
+        X0[h] = pack_bf16x2(acc[i][2 * q2][4 * r4 + 2 * h], acc[i][2 * q2][4 * r4 + 2 * h + 1]);
+        X1[h] = pack_bf16x2(acc[i][2 * q2 + 1][4 * r4 + 2 * h], acc[i][2 * q2 + 1][4 * r4 + 2 * h + 1]);
       }
       if constexpr (SECTION < 2) {
         const f32x4_t c = *reinterpret_cast<const f32x4_t*>(p.cos_t + pc * kHeadDim + d0);
         const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(p.sin_t + pc * kHeadDim + d0);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          // x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1], each op rounded to bf16
-          const float y0 = bf16r(bf16r(x0[t] * c[t]) + bf16r(-x1[t] * sn[t]));
-          const float y1 = bf16r(bf16r(x1[t] * c[t]) + bf16r(x0[t] * sn[t]));
-          x0[t] = y0;
-          x1[t] = y1;
+        for (int h = 0; h < 2; ++h) {
+          // x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1], each op rounded
+          // to bf16; bf16(-x2*s) = -bf16(x2*s) (round-to-nearest-even is symmetric)
+          const float a0 = bf16lo(X0[h]), a1 = bf16hi(X0[h]);
+          const float b0 = bf16lo(X1[h]), b1 = bf16hi(X1[h]);
+          const float c0 = c[2 * h], c1 = c[2 * h + 1], s0 = sn[2 * h], s1 = sn[2 * h + 1];
+          const uint32_t ac = pack_bf16x2(a0 * c0, a1 * c1), bs = pack_bf16x2(b0 * s0, b1 * s1);
+          const uint32_t bc = pack_bf16x2(b0 * c0, b1 * c1), as = pack_bf16x2(a0 * s0, a1 * s1);
+          X0[h] = pack_bf16x2(bf16lo(ac) - bf16lo(bs), bf16hi(ac) - bf16hi(bs));
+          X1[h] = pack_bf16x2(bf16lo(bc) + bf16lo(as), bf16hi(bc) + bf16hi(as));
         }
       }
-      const u32x2_t lo = {pack_bf16x2(x0[0], x0[1]), pack_bf16x2(x0[2], x0[3])};
-      const u32x2_t hi = {pack_bf16x2(x1[0], x1[1]), pack_bf16x2(x1[2], x1[3])};
+      const u32x2_t lo = {X0[0], X0[1]};
+      const u32x2_t hi = {X1[0], X1[1]};
       if constexpr (SECTION == 0) {
         uint16_t* qp = p.q_out + static_cast<int64_t>(m) * HD + head * kHeadDim + d0;
         *reinterpret_cast<u32x2_t*>(qp) = lo;
@@ -184,8 +186,8 @@ __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const 
       } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          kv[(d0 + t) * kPageSize + slot] = static_cast<uint16_t>(f32_to_bf16(x0[t]));
-          kv[(d0 + 32 + t) * kPageSize + slot] = static_cast<uint16_t>(f32_to_bf16(x1[t]));
+          kv[(d0 + t) * kPageSize + slot] = static_cast<uint16_t>(X0[t >> 1] >> (16 * (t & 1)));
+          kv[(d0 + 32 + t) * kPageSize + slot] = static_cast<uint16_t>(X1[t >> 1] >> (16 * (t & 1)));
         }
       }
     }
@@ -823,13 +825,17 @@ int launch_tile(const GemmParams& p, hipStream_t st) {
 template <class T, int EPI, int AM, int NS = 2>
 int launch_dl(const GemmParams& p, hipStream_t st) {
   using L = DlLayout<T, NS>;
-  static bool lds_set = false;  // the attribute is per kernel; setting it twice is harmless
-  if (!lds_set) {
+  // The dynamic-LDS limit is raised once per kernel and device (setting it
+  // twice, e.g. from two threads, is harmless).
+  static bool lds_set[64] = {false};
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= 64 || !lds_set[dev]) {
     if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dl_kernel<T, EPI, AM, NS>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS),
                            "gemm_dl_kernel LDS attribute"))
       return rc;
-    lds_set = true;
+    if (dev >= 0 && dev < 64) lds_set[dev] = true;
   }
   const dim3 grid((p.N + T::BN - 1) / T::BN, (p.M + T::BM - 1) / T::BM), block(T::THREADS);
   hipLaunchKernelGGL((gemm_dl_kernel<T, EPI, AM, NS>), grid, block, L::LDS, st, p);
