@@ -178,8 +178,13 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
       ac += __builtin_amdgcn_exp2f(__builtin_fmaf(fc[e], kLog2e, -mcs));
       if (kHasU) au += __builtin_amdgcn_exp2f(__builtin_fmaf(fu[e], kLog2e, -mus));
     }
-    sc = merge_stats(sc, RowStats{mc, ac});
-    if (kHasU) su = merge_stats(su, RowStats{mu, au});
+    if (base == 0) {  // the first pass starts the statistics (V = 8194 has one full pass)
+      sc = RowStats{mc, ac};
+      if (kHasU) su = RowStats{mu, au};
+    } else {
+      sc = merge_stats(sc, RowStats{mc, ac});
+      if (kHasU) su = merge_stats(su, RowStats{mu, au});
+    }
     // argmax; the first maximum in index order wins, as torch.argmax does:
     // the maximum by a max3 tree, then the lowest element equal to it (the
     // guided values reuse the registers of fc, which are dead by now).
@@ -228,33 +233,59 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
   }
   Best best{best_g, best_v, 0.f, 0.f};
 
-  // Wave reduction, then across the four waves through LDS.
+  // Block reductions.  The softmax denominators: first the block maximum
+  // (max only), then every thread rescales its partial sum once to it and the
+  // partial sums are added -- two exps per thread instead of a (max, sum)
+  // merge with two exps at every reduction step.  The argmax rides along with
+  // the maximum.
+  const int wave = tid >> 6;
+  float mcw = sc.m, muw = su.m;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
-    sc = merge_stats(sc, RowStats{shfl_xor_f(sc.m, m), shfl_xor_f(sc.s, m)});
-    su = merge_stats(su, RowStats{shfl_xor_f(su.m, m), shfl_xor_f(su.s, m)});
+    mcw = fmaxf(mcw, shfl_xor_f(mcw, m));
+    if (kHasU) muw = fmaxf(muw, shfl_xor_f(muw, m));
     const Best o{shfl_xor_f(best.g, m), shfl_xor_i(best.idx, m), 0.f, 0.f};
     if (better(o, best)) best = o;
   }
   __shared__ float s_f[kThreads / 64][5];
   __shared__ int s_i[kThreads / 64];
-  const int wave = tid >> 6;
   if ((tid & 63) == 0) {
-    s_f[wave][0] = sc.m;
-    s_f[wave][1] = sc.s;
-    s_f[wave][2] = su.m;
-    s_f[wave][3] = su.s;
+    s_f[wave][0] = mcw;
+    s_f[wave][1] = muw;
     s_f[wave][4] = best.g;
     s_i[wave] = best.idx;
   }
   __syncthreads();
+  float Mc = s_f[0][0], Mu = s_f[0][1];
+#pragma unroll
+  for (int q = 1; q < kThreads / 64; ++q) {
+    Mc = fmaxf(Mc, s_f[q][0]);
+    Mu = fmaxf(Mu, s_f[q][1]);
+  }
+  // a thread with no finite value (m = -inf) contributes nothing; so does a
+  // row whose maximum is -inf, whose sum stays 0 as in merge_stats
+  float tc = sc.m == -INFINITY ? 0.f : sc.s * __builtin_amdgcn_exp2f((sc.m - Mc) * kLog2e);
+  float tu = (!kHasU || su.m == -INFINITY) ? 0.f : su.s * __builtin_amdgcn_exp2f((su.m - Mu) * kLog2e);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    tc += shfl_xor_f(tc, m);
+    if (kHasU) tu += shfl_xor_f(tu, m);
+  }
+  if ((tid & 63) == 0) {
+    s_f[wave][2] = tc;
+    s_f[wave][3] = tu;
+  }
+  __syncthreads();
   if (tid == 0) {
+    float Sc = s_f[0][2], Su = s_f[0][3];
     for (int q = 1; q < kThreads / 64; ++q) {
-      sc = merge_stats(sc, RowStats{s_f[q][0], s_f[q][1]});
-      su = merge_stats(su, RowStats{s_f[q][2], s_f[q][3]});
+      Sc += s_f[q][2];
+      Su += s_f[q][3];
       const Best o{s_f[q][4], s_i[q], 0.f, 0.f};
       if (better(o, best)) best = o;
     }
+    sc = RowStats{Mc, Sc};
+    su = RowStats{Mu, Su};
     const int x = best.idx < V ? best.idx : 0;  // a row of only -inf / NaN scores: token 0, as torch.argmax
     const float lpr = P.log_prior[x];
     // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
