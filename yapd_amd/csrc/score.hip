@@ -94,11 +94,59 @@ __device__ __forceinline__ bool better(const Best& o, const Best& cur) {
   return o.g > cur.g || (o.g == cur.g && o.idx < cur.idx);
 }
 
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
-__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Wave reductions on DPP: within each 16-lane row the two quad permutes, the
+// half-row mirror and the row mirror leave the row's result in all of its
+// lanes; the four row results are then combined from SGPRs (readlane), so
+// every lane ends with the wave's result and no LDS permute is issued.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp_f<kDppQuadXor1>(v));
+  v = op(v, dpp_f<kDppQuadXor2>(v));
+  v = op(v, dpp_f<kDppHalfMirror>(v));
+  v = op(v, dpp_f<kDppMirror>(v));
+  return op(op(readlane_f(v, 0), readlane_f(v, 16)), op(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// The argmax (value, lowest index) of a wave, in every lane.
+__device__ __forceinline__ Best wave_best(Best b) {
+  {
+    const Best o{dpp_f<kDppQuadXor1>(b.g), dpp_i<kDppQuadXor1>(b.idx), 0.f, 0.f};
+    if (better(o, b)) b = o;
+  }
+  {
+    const Best o{dpp_f<kDppQuadXor2>(b.g), dpp_i<kDppQuadXor2>(b.idx), 0.f, 0.f};
+    if (better(o, b)) b = o;
+  }
+  {
+    const Best o{dpp_f<kDppHalfMirror>(b.g), dpp_i<kDppHalfMirror>(b.idx), 0.f, 0.f};
+    if (better(o, b)) b = o;
+  }
+  {
+    const Best o{dpp_f<kDppMirror>(b.g), dpp_i<kDppMirror>(b.idx), 0.f, 0.f};
+    if (better(o, b)) b = o;
+  }
+  Best r{readlane_f(b.g, 0), __builtin_amdgcn_readlane(b.idx, 0), 0.f, 0.f};
+#pragma unroll
+  for (int q = 16; q < 64; q += 16) {
+    const Best o{readlane_f(b.g, q), __builtin_amdgcn_readlane(b.idx, q), 0.f, 0.f};
+    if (better(o, r)) r = o;
+  }
+  return r;
 }
 
 // Streaming pass for one (pair, position).  Per element the VALU work is
@@ -239,14 +287,10 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
   // merge with two exps at every reduction step.  The argmax rides along with
   // the maximum.
   const int wave = tid >> 6;
-  float mcw = sc.m, muw = su.m;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    mcw = fmaxf(mcw, shfl_xor_f(mcw, m));
-    if (kHasU) muw = fmaxf(muw, shfl_xor_f(muw, m));
-    const Best o{shfl_xor_f(best.g, m), shfl_xor_i(best.idx, m), 0.f, 0.f};
-    if (better(o, best)) best = o;
-  }
+  auto fmax_op = [](float a, float b) { return fmaxf(a, b); };
+  const float mcw = wave_reduce(sc.m, fmax_op);
+  const float muw = kHasU ? wave_reduce(su.m, fmax_op) : 0.f;
+  best = wave_best(best);
   __shared__ float s_f[kThreads / 64][5];
   __shared__ int s_i[kThreads / 64];
   if ((tid & 63) == 0) {
@@ -266,11 +310,9 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
   // row whose maximum is -inf, whose sum stays 0 as in merge_stats
   float tc = sc.m == -INFINITY ? 0.f : sc.s * __builtin_amdgcn_exp2f((sc.m - Mc) * kLog2e);
   float tu = (!kHasU || su.m == -INFINITY) ? 0.f : su.s * __builtin_amdgcn_exp2f((su.m - Mu) * kLog2e);
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    tc += shfl_xor_f(tc, m);
-    if (kHasU) tu += shfl_xor_f(tu, m);
-  }
+  auto add_op = [](float a, float b) { return a + b; };
+  tc = wave_reduce(tc, add_op);
+  if (kHasU) tu = wave_reduce(tu, add_op);
   if ((tid & 63) == 0) {
     s_f[wave][2] = tc;
     s_f[wave][3] = tu;
