@@ -58,7 +58,8 @@ int yapd_abi_version(void);
  * (server/engine.py:559-561; the reference adds it unscaled).
  * Outputs [n_pairs, bl]: sampled (int64), pmi (fp32), unmask (u8), xt_out
  * (int64); per pair: n_mask_after (int32), hit_eos (u8).  1 <= bl <= 64, 1 <= K <= 64.
- * Two launches: a streaming pass per (pair, position), then one wave per pair.
+ * One launch: a workgroup per pair, one wave per position, then the pair's
+ * decision by one wave from LDS.
  * ------------------------------------------------------------------------ */
 
 int yapd_score_cfg_pmi_unmask(

@@ -18,8 +18,8 @@
 namespace yapd {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 16;  // dwords per row per thread per full pass (V = 8194: one pass + 1 dword)
+constexpr int kPairWaves = 16;  // waves per workgroup; one workgroup per CFG pair
+constexpr int kUnroll = 16;    // dwords per row per lane per pass (V = 8194: four passes + 1 dword)
 
 struct ScoreParams {
   const uint16_t* logits;
@@ -149,16 +149,17 @@ __device__ __forceinline__ Best wave_best(Best b) {
   return r;
 }
 
-// Streaming pass for one (pair, position).  Per element the VALU work is
-// kept to the minimum the math needs (bf16 unpack, max, one FMA + v_exp and an
-// add per branch, the guided score and a compare/select for the argmax):
-// with 268 MB of logits this kernel sits at the VALU/HBM balance point.
-template <bool kHasU, bool kSample, bool kRank = false>
-__global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams P) {
-  const int item = blockIdx.x;
-  const int pair = item / P.bl;
-  const int pos = item - pair * P.bl;
-  const int tid = threadIdx.x;
+// One (pair, position) scored by one wave: a streaming pass over the cond
+// and null rows (dword loads; rows are only 4-byte aligned at V = 8194), each
+// lane keeping running softmax statistics and its argmax, then wave
+// reductions on DPP.  Per element the VALU work is what the math needs (bf16
+// unpack, max, one FMA + v_exp and an add per branch, the guided score and a
+// compare/select for the argmax).  A pass's 32 loads per lane are issued back
+// to back; the other waves of the workgroup (4 per SIMD) cover their latency.
+// Returns the token (every lane) and the pmi (lane 0).
+template <bool kHasU, bool kSample, bool kRank>
+__device__ __forceinline__ void score_item(const ScoreParams& P, int item, int pair, int pos, int lane, int& x_out,
+                                           float& pmi_out) {
   const int64_t crow = static_cast<int64_t>(P.cond_row0) + static_cast<int64_t>(pair) * P.pair_row_step;
   const uint16_t* rc = P.logits + crow * P.seq_stride + static_cast<int64_t>(pos) * P.pos_stride;
   const uint16_t* ru = rc + static_cast<int64_t>(P.null_row_offset) * P.seq_stride;
@@ -170,6 +171,7 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
   const uint32_t key0 = static_cast<uint32_t>(P.seed), key1 = static_cast<uint32_t>(P.seed >> 32);
   const uint32_t off0 = static_cast<uint32_t>(P.rng_offset), off1 = static_cast<uint32_t>(P.rng_offset >> 32);
   constexpr float kLog2e = 1.4426950408889634f;
+  constexpr int kPass = 64 * kUnroll;  // dwords per row per pass
 
   RowStats sc{-INFINITY, 0.f}, su{-INFINITY, 0.f};
   float best_g = -INFINITY;
@@ -191,18 +193,30 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
     }
     return g;
   };
+  // Running statistics of one branch after a pass with maximum mp and values
+  // f: one rescale exp, then the pass's exps against the new maximum (a
+  // maximum of -inf keeps the sum at 0).
+  auto update = [&](RowStats& st, float mp, const float* f) {
+    const float mn = fmaxf(st.m, mp);
+    const float mns = mn == -INFINITY ? 0.f : mn * kLog2e;
+    float acc = st.m == -INFINITY ? 0.f : st.s * __builtin_amdgcn_exp2f(st.m * kLog2e - mns);
+#pragma unroll
+    for (int e = 0; e < 2 * kUnroll; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(f[e], kLog2e, -mns));
+    st = RowStats{mn, acc};
+  };
 
-  // Full passes: every thread owns kUnroll dwords per row, loads issued back to back.
-  int base = 0;
-  for (; base + kThreads * kUnroll <= nw; base += kThreads * kUnroll) {
-    uint32_t xc[kUnroll], xu[kUnroll];
-    const uint32_t* pc = wc + base + tid;
-    const uint32_t* pu = wu + base + tid;
+  const int n_pass = nw / kPass;
+  uint32_t xc[kUnroll], xu[kUnroll];
+  auto load_pass = [&](int base) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      xc[u] = pc[u * kThreads];
-      if (kHasU) xu[u] = pu[u * kThreads];
+      xc[u] = wc[base + u * 64 + lane];
+      if (kHasU) xu[u] = wu[base + u * 64 + lane];
     }
+  };
+  for (int pi = 0; pi < n_pass; ++pi) {
+    const int base = pi * kPass;
+    load_pass(base);
     float fc[2 * kUnroll], fu[2 * kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -219,46 +233,34 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
       mc = fmaxf(mc, fc[e]);
       if (kHasU) mu = fmaxf(mu, fu[e]);
     }
-    const float mcs = mc * kLog2e, mus = mu * kLog2e;
-    float ac = 0.f, au = 0.f;
-#pragma unroll
-    for (int e = 0; e < 2 * kUnroll; ++e) {
-      ac += __builtin_amdgcn_exp2f(__builtin_fmaf(fc[e], kLog2e, -mcs));
-      if (kHasU) au += __builtin_amdgcn_exp2f(__builtin_fmaf(fu[e], kLog2e, -mus));
-    }
-    if (base == 0) {  // the first pass starts the statistics (V = 8194 has one full pass)
-      sc = RowStats{mc, ac};
-      if (kHasU) su = RowStats{mu, au};
-    } else {
-      sc = merge_stats(sc, RowStats{mc, ac});
-      if (kHasU) su = merge_stats(su, RowStats{mu, au});
-    }
+    update(sc, mc, fc);
+    if (kHasU) update(su, mu, fu);
     // argmax; the first maximum in index order wins, as torch.argmax does:
     // the maximum by a max3 tree, then the lowest element equal to it (the
     // guided values reuse the registers of fc, which are dead by now).
     float gv[2 * kUnroll];
 #pragma unroll
     for (int e = 0; e < 2 * kUnroll; ++e)
-      gv[e] = guided(fc[e], kHasU ? fu[e] : 0.f, 2 * (base + (e >> 1) * kThreads + tid) + (e & 1));
+      gv[e] = guided(fc[e], kHasU ? fu[e] : 0.f, 2 * (base + (e >> 1) * 64 + lane) + (e & 1));
     float pg = gv[0];
 #pragma unroll
     for (int e = 1; e < 2 * kUnroll; ++e) pg = fmaxf(pg, gv[e]);
-    int pe = 0;
-#pragma unroll
-    for (int e = 2 * kUnroll - 1; e >= 0; --e) pe = gv[e] == pg ? e : pe;
     if (pg > best_g) {
+      int pe = 0;
+#pragma unroll
+      for (int e = 2 * kUnroll - 1; e >= 0; --e) pe = gv[e] == pg ? e : pe;
       best_g = pg;
-      best_v = 2 * (base + (pe >> 1) * kThreads + tid) + (pe & 1);
+      best_v = 2 * (base + (pe >> 1) * 64 + lane) + (pe & 1);
     }
   }
-  // Tail: the remaining dwords, one per thread at a time.
-  for (int j = base + tid; j < nw; j += kThreads) {
-    const uint32_t xc = wc[j];
-    const uint32_t xu = kHasU ? wu[j] : 0u;
+  // Tail: the remaining dwords, one per lane at a time.
+  for (int j = n_pass * kPass + lane; j < nw; j += 64) {
+    const uint32_t tc = wc[j];
+    const uint32_t tu = kHasU ? wu[j] : 0u;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const float lc = h ? bf16hi(xc) : bf16lo(xc);
-      const float lu = h ? bf16hi(xu) : bf16lo(xu);
+      const float lc = h ? bf16hi(tc) : bf16lo(tc);
+      const float lu = h ? bf16hi(tu) : bf16lo(tu);
       sc = merge_stats(sc, RowStats{lc, 1.f});
       if (kHasU) su = merge_stats(su, RowStats{lu, 1.f});
       const float g = guided(lc, lu, 2 * j + h);
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
       }
     }
   }
-  if ((V & 1) && tid == 0) {  // odd vocab: the last element sits alone
+  if ((V & 1) && lane == 0) {  // odd vocab: the last element sits alone
     const float lc = bf16_to_f32(rc[V - 1]);
     const float lu = kHasU ? bf16_to_f32(ru[V - 1]) : 0.f;
     sc = merge_stats(sc, RowStats{lc, 1.f});
@@ -279,63 +281,31 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
       best_v = V - 1;
     }
   }
-  Best best{best_g, best_v, 0.f, 0.f};
 
-  // Block reductions.  The softmax denominators: first the block maximum
-  // (max only), then every thread rescales its partial sum once to it and the
-  // partial sums are added -- two exps per thread instead of a (max, sum)
-  // merge with two exps at every reduction step.  The argmax rides along with
-  // the maximum.
-  const int wave = tid >> 6;
+  // Wave reductions: the maximum of each branch (with the argmax), then each
+  // lane rescales its sum once to it and the sums are added.
   auto fmax_op = [](float a, float b) { return fmaxf(a, b); };
-  const float mcw = wave_reduce(sc.m, fmax_op);
-  const float muw = kHasU ? wave_reduce(su.m, fmax_op) : 0.f;
-  best = wave_best(best);
-  __shared__ float s_f[kThreads / 64][5];
-  __shared__ int s_i[kThreads / 64];
-  if ((tid & 63) == 0) {
-    s_f[wave][0] = mcw;
-    s_f[wave][1] = muw;
-    s_f[wave][4] = best.g;
-    s_i[wave] = best.idx;
-  }
-  __syncthreads();
-  float Mc = s_f[0][0], Mu = s_f[0][1];
-#pragma unroll
-  for (int q = 1; q < kThreads / 64; ++q) {
-    Mc = fmaxf(Mc, s_f[q][0]);
-    Mu = fmaxf(Mu, s_f[q][1]);
-  }
-  // a thread with no finite value (m = -inf) contributes nothing; so does a
-  // row whose maximum is -inf, whose sum stays 0 as in merge_stats
-  float tc = sc.m == -INFINITY ? 0.f : sc.s * __builtin_amdgcn_exp2f((sc.m - Mc) * kLog2e);
-  float tu = (!kHasU || su.m == -INFINITY) ? 0.f : su.s * __builtin_amdgcn_exp2f((su.m - Mu) * kLog2e);
   auto add_op = [](float a, float b) { return a + b; };
-  tc = wave_reduce(tc, add_op);
-  if (kHasU) tu = wave_reduce(tu, add_op);
-  if ((tid & 63) == 0) {
-    s_f[wave][2] = tc;
-    s_f[wave][3] = tu;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float Sc = s_f[0][2], Su = s_f[0][3];
-    for (int q = 1; q < kThreads / 64; ++q) {
-      Sc += s_f[q][2];
-      Su += s_f[q][3];
-      const Best o{s_f[q][4], s_i[q], 0.f, 0.f};
-      if (better(o, best)) best = o;
-    }
-    sc = RowStats{Mc, Sc};
-    su = RowStats{Mu, Su};
-    const int x = best.idx < V ? best.idx : 0;  // a row of only -inf / NaN scores: token 0, as torch.argmax
+  const float Mc = wave_reduce(sc.m, fmax_op);
+  const float Mu = kHasU ? wave_reduce(su.m, fmax_op) : 0.f;
+  const Best best = wave_best(Best{best_g, best_v, 0.f, 0.f});
+  // a lane with no finite value (m = -inf) contributes nothing; so does a row
+  // whose maximum is -inf, whose sum stays 0
+  const float Sc = wave_reduce(sc.m == -INFINITY ? 0.f : sc.s * __builtin_amdgcn_exp2f((sc.m - Mc) * kLog2e), add_op);
+  const float Su = kHasU ? wave_reduce(su.m == -INFINITY ? 0.f : su.s * __builtin_amdgcn_exp2f((su.m - Mu) * kLog2e),
+                                       add_op)
+                         : 0.f;
+  const int x = best.idx < V ? best.idx : 0;  // a row of only -inf / NaN scores: token 0, as torch.argmax
+  x_out = x;
+  pmi_out = 0.f;
+  if (lane == 0) {
     const float lpr = P.log_prior[x];
     // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
     const float lcx = bf16_to_f32(rc[x]);
-    float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lcx - sc.m), sc.s), 1e-8f)), lpr);
+    float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lcx - Mc), Sc), 1e-8f)), lpr);
     if (kHasU) {
       const float lux = bf16_to_f32(ru[x]);
-      const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lux - su.m), su.s), 1e-8f)), lpr);
+      const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lux - Mu), Su), 1e-8f)), lpr);
       pmi = __fsub_rn(__fmul_rn(w1, pmi), __fmul_rn(w, pmi_u));
     }
     if (P.pos_gumbel) {
@@ -345,28 +315,42 @@ __global__ __launch_bounds__(kThreads) void score_items_kernel(const ScoreParams
         pmi = __fadd_rn(pmi, gumbel_from_u32(r.x));
       }
     }
-    P.sampled[item] = x;
-    P.pmi[item] = pmi;
+    pmi_out = pmi;
   }
 }
 
-// One wave per pair: the decision rule of server/engine.py:563-593.
-__global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParams P) {
-  const int pair = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (pair >= P.n_pairs) return;
+// The per-pair inputs of the decision rule, one entry per lane: every load is
+// independent, and the step tables are picked by readlane once k is known.
+struct PairInputs {
+  int64_t k;
+  float q_lane;
+  int sched_lane;
+  bool act;
+  int64_t xt;
+};
+
+__device__ __forceinline__ PairInputs load_pair_inputs(const ScoreParams& P, int pair, int lane) {
+  const int64_t ib = static_cast<int64_t>(pair) * P.bl;
+  PairInputs in;
+  in.k = P.k_step[pair];
+  in.q_lane = lane < P.K ? P.q_tab[lane] : 0.f;
+  in.sched_lane = lane < P.K ? P.sched[lane] : 0;
+  in.act = P.active == nullptr || P.active[pair] != 0;
+  in.xt = lane < P.bl ? P.xt_in[ib + lane] : 0;
+  return in;
+}
+
+// The decision rule of server/engine.py:563-593 for one pair, one wave, lane
+// = position: rank by pairwise compare (ties -> lowest position), p =
+// q_k (m-1), linear quantile, n = min(max(min(sched, m), n_quant), m), top-n
+// unmask, n_mask_after and hit_eos.
+__device__ __forceinline__ void decide_pair(const ScoreParams& P, int pair, int lane, const PairInputs& in, float key,
+                                            int64_t smp) {
   const int bl = P.bl;
-  const int lane = threadIdx.x & 63;
   const int64_t ib = static_cast<int64_t>(pair) * bl;
   const bool valid = lane < bl;
-  // Every load is independent of every other: the step tables come in
-  // lane-parallel (entry `lane`) and are picked by readlane once k is known.
-  const int64_t k = P.k_step[pair];
-  const float q_lane = lane < P.K ? P.q_tab[lane] : 0.f;
-  const int sched_lane = lane < P.K ? P.sched[lane] : 0;
-  const bool act = P.active == nullptr || P.active[pair] != 0;
-  const int64_t xt = valid ? P.xt_in[ib + lane] : 0;
-  const float key = valid ? P.pmi[ib + lane] : 0.f;
-  const int64_t smp = valid ? P.sampled[ib + lane] : 0;
+  const int64_t k = in.k;
+  const int64_t xt = in.xt;
   const bool msk = valid && xt == P.mask_id;
   const uint64_t bal = __ballot(msk);
   const int m = __popcll(bal);
@@ -382,7 +366,7 @@ __global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParam
   int kc = k < P.K - 1 ? static_cast<int>(k) : P.K - 1;
   kc = kc < 0 ? 0 : kc;
   // p = q_t[k] * (m-1).clamp_min(0).float(); lo/hi = floor/ceil; linear interpolation.
-  const float p = __fmul_rn(readlane_f(q_lane, kc), static_cast<float>(m > 1 ? m - 1 : 0));
+  const float p = __fmul_rn(readlane_f(in.q_lane, kc), static_cast<float>(m > 1 ? m - 1 : 0));
   int lo = static_cast<int>(floorf(p));
   int hi = static_cast<int>(ceilf(p));
   lo = lo < 0 ? 0 : lo;
@@ -393,11 +377,11 @@ __global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParam
   const float v_hi = bhi ? readlane_f(key, __ffsll(static_cast<unsigned long long>(bhi)) - 1) : INFINITY;
   const float tau = __fadd_rn(v_lo, __fmul_rn(__fsub_rn(p, static_cast<float>(lo)), __fsub_rn(v_hi, v_lo)));
   const int n_quant = P.quantile_on ? __popcll(__ballot(msk && key >= tau)) : 0;
-  const int n_sched = min(__builtin_amdgcn_readlane(sched_lane, kc), m);
+  const int n_sched = min(__builtin_amdgcn_readlane(in.sched_lane, kc), m);
   int n = min(max(n_sched, n_quant), m);
   if (k >= P.K - 1) n = m;
   if (m == 0) n = 0;
-  const bool unm = act && msk && desc < n;
+  const bool unm = in.act && msk && desc < n;
   const int64_t xo = unm ? smp : xt;
   if (valid) {
     P.unmask[ib + lane] = unm ? 1 : 0;
@@ -408,6 +392,36 @@ __global__ __launch_bounds__(kThreads) void score_decide_kernel(const ScoreParam
   if (lane == 0) {
     P.n_mask_after[pair] = n_after;
     P.hit_eos[pair] = eos ? 1 : 0;
+  }
+}
+
+// One workgroup per pair: wave w scores positions w, w + kPairWaves, ..., and
+// wave 0 then applies the decision rule to the pair's keys from LDS -- one
+// launch, no handoff through global memory between workgroups.
+template <bool kHasU, bool kSample, bool kRank = false>
+__global__ __launch_bounds__(64 * kPairWaves) void score_pair_kernel(const ScoreParams P) {
+  const int pair = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ float s_key[64];
+  __shared__ int64_t s_smp[64];
+  PairInputs in{};
+  if (wave == 0) in = load_pair_inputs(P, pair, lane);  // in flight while wave 0 scores
+  for (int pos = wave; pos < P.bl; pos += kPairWaves) {
+    const int item = pair * P.bl + pos;
+    int x;
+    float pmi;
+    score_item<kHasU, kSample, kRank>(P, item, pair, pos, lane, x, pmi);
+    if (lane == 0) {
+      P.sampled[item] = x;
+      P.pmi[item] = pmi;
+      s_key[pos] = pmi;
+      s_smp[pos] = x;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const bool valid = lane < P.bl;
+    decide_pair(P, pair, lane, in, valid ? s_key[lane] : 0.f, valid ? s_smp[lane] : 0);
   }
 }
 
@@ -471,21 +485,17 @@ extern "C" int yapd_score_cfg_pmi_unmask(
   P.n_mask_after = n_mask_after_out;
   P.hit_eos = hit_eos_out;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(n_pairs * bl), block(yapd::kThreads);
+  const dim3 grid(n_pairs), block(64 * yapd::kPairWaves);
   if (has_uncond && temperature > 0.f)
-    hipLaunchKernelGGL((yapd::score_items_kernel<true, true>), grid, block, 0, st, P);
+    hipLaunchKernelGGL((yapd::score_pair_kernel<true, true>), grid, block, 0, st, P);
   else if (has_uncond && cfg_w > 0.f)
-    hipLaunchKernelGGL((yapd::score_items_kernel<true, false, true>), grid, block, 0, st, P);
+    hipLaunchKernelGGL((yapd::score_pair_kernel<true, false, true>), grid, block, 0, st, P);
   else if (has_uncond)
-    hipLaunchKernelGGL((yapd::score_items_kernel<true, false>), grid, block, 0, st, P);
+    hipLaunchKernelGGL((yapd::score_pair_kernel<true, false>), grid, block, 0, st, P);
   else if (temperature > 0.f)
-    hipLaunchKernelGGL((yapd::score_items_kernel<false, true>), grid, block, 0, st, P);
+    hipLaunchKernelGGL((yapd::score_pair_kernel<false, true>), grid, block, 0, st, P);
   else
-    hipLaunchKernelGGL((yapd::score_items_kernel<false, false>), grid, block, 0, st, P);
-  YAPD_LAUNCH_CHECK("score_items_kernel launch");
-  const int waves_per_block = yapd::kThreads / 64;
-  hipLaunchKernelGGL(yapd::score_decide_kernel, dim3((n_pairs + waves_per_block - 1) / waves_per_block),
-                     dim3(yapd::kThreads), 0, st, P);
-  YAPD_LAUNCH_CHECK("score_decide_kernel launch");
+    hipLaunchKernelGGL((yapd::score_pair_kernel<false, false>), grid, block, 0, st, P);
+  YAPD_LAUNCH_CHECK("score_pair_kernel launch");
   return YAPD_OK;
 }
