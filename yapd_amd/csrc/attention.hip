@@ -63,7 +63,28 @@ __device__ __forceinline__ u32x4_t load16_stream(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
 }
 
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+// Lane l combined with lane l ^ 16 (l ^ 32): v_permlane16_swap (32_swap) of a
+// value with itself returns the two halves of every exchanged pair, so the
+// max or sum of its two results is the pair's in both lanes -- a VALU
+// exchange instead of an LDS permute.
+__device__ __forceinline__ float2 swap16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor16_32(float v) {
+  const float2 a = swap16(v);
+  const float2 b = swap32(fmaxf(a.x, a.y));
+  return fmaxf(b.x, b.y);
+}
+__device__ __forceinline__ float sum_xor16_32(float v) {
+  const float2 a = swap16(v);
+  const float2 b = swap32(a.x + a.y);
+  return b.x + b.y;
+}
 
 template <int NQT>
 __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParams P) {
@@ -192,8 +213,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
       float cm = sv[0];
 #pragma unroll
       for (int i = 1; i < 8; ++i) cm = fmaxf(cm, sv[i]);
-      cm = fmaxf(cm, shfl_xor_f(cm, 16));
-      cm = fmaxf(cm, shfl_xor_f(cm, 32));
+      cm = max_xor16_32(cm);
       const float mn = fmaxf(m[qt], cm);
       const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
       float ps = 0.f;
@@ -227,9 +247,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
   // o[qt][mt][j] = O^T[hd = 16mt + 4g + j][q = qt*16 + n]
 #pragma unroll
   for (int qt = 0; qt < NQT; ++qt) {
-    float L = l[qt];
-    L += shfl_xor_f(L, 16);
-    L += shfl_xor_f(L, 32);
+    const float L = sum_xor16_32(l[qt]);
     const int q = qt * 16 + n;
     if (q >= bl) continue;
     const int64_t row_q = (static_cast<int64_t>(r) * bl + q) * H + h;
