@@ -124,15 +124,16 @@ def test_full_scoring_shape(dev):
 
 @pytest.mark.parametrize("n_pairs,bl,V,cfg", [(96, 32, 8194, 0.5), (40, 32, 8192, 0.5), (33, 32, 8704, 0.5),
                                                (40, 32, 8194, 0.0)])
-def test_pipelined_items_kernel(dev, n_pairs, bl, V, cfg):
-    # Rows of 4096..4352 dwords take the software-pipelined streaming kernel,
-    # whose workgroups each walk several items (more items than 4 per CU):
-    # V = 8192 has no tail dword, V = 8704 gives every thread one.
+def test_pass_and_tail_structure(dev, n_pairs, bl, V, cfg):
+    # A wave streams a row in passes of 1024 dwords, then a per-lane tail:
+    # V = 8194 is four passes and one tail dword, V = 8192 four passes and no
+    # tail, V = 8704 four passes and four tail dwords per lane; cfg = 0 runs
+    # the single-branch kernel.
     res, ref, _ = run_both(dev, n_pairs=n_pairs, bl=bl, V=V, seed=V + n_pairs, cfg=cfg, layout="stacked")
     assert_exact(res, ref)
 
 
-def test_pipelined_sampling_replays_streams(dev):
+def test_sampling_replays_streams_at_scale(dev):
     res, ref, _ = run_both(dev, n_pairs=64, bl=32, V=8194, seed=4, temperature=0.6, pos_noise=True, tau=3.0)
     agree = (res.sampled.cpu() == ref["sampled"]).float().mean().item()
     assert agree >= 0.98
