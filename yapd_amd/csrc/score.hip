@@ -1,16 +1,18 @@
 // (c) CFG combine + prior-calibrated PMI + time-shifted-quantile unmask.
 //
-// One 256-thread workgroup per (pair, position) streams the cond and null
-// logit rows once from HBM (dword loads; rows are only 4-byte aligned since
-// V = 8194), keeping an online (max, sum-exp) per branch and the argmax of
-// the guided score.  The guided argmax uses (1+w)*lc - w*lu, which differs
-// from the reference's lsc + w*(lsc - lsu) (server/engine.py:536-539) only by
-// a per-row constant.  A second, tiny kernel (one wave per pair) then runs the
-// per-pair decision rule of server/engine.py:563-593: ranks by pairwise
-// comparison, the linear quantile with the reference's fp32 op order, top-n
-// unmask.  Two launches instead of a "last workgroup finishes the pair"
-// handoff: on a multi-XCD part each agent-scope release/acquire fence writes
-// back / invalidates the XCD's L2, which costs far more than a launch.
+// One workgroup of 16 waves per CFG pair.  Each wave scores whole positions:
+// it streams the position's cond and null logit rows once from HBM (dword
+// loads; rows are only 4-byte aligned since V = 8194), each lane keeping a
+// running (max, sum-exp) per branch and the argmax of the guided score, then
+// reduces across the wave on DPP.  The guided argmax uses (1+w)*lc - w*lu,
+// which differs from the reference's lsc + w*(lsc - lsu)
+// (server/engine.py:536-539) only by a per-row constant.  The pair's keys go
+// to LDS and one wave runs the per-pair decision rule of
+// server/engine.py:563-593: ranks by pairwise comparison, the linear quantile
+// with the reference's fp32 op order, top-n unmask.  Keeping the pair in one
+// workgroup makes the handoff an LDS barrier: across workgroups it would need
+// agent-scope release/acquire fences, which on a multi-XCD part write back /
+// invalidate the XCD's L2, or a second launch.
 #include <cmath>
 
 #include "common.h"
