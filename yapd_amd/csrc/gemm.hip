@@ -575,7 +575,10 @@ struct DlLayout {
   static constexpr int WAVES = T::THREADS / 64;
   static_assert(NS == 2 || (WAVES == 1 && NS >= 2 && NS <= 4), "more than two stages need a one-wave tile");
   static constexpr int ROWB = 128;
+  static constexpr int CPR = 8;  // 16-byte chunks per row
+  static constexpr int RPI = 8;  // rows per 1 KB load instruction
   static constexpr int A_BYTES = T::BM * ROWB, B_BYTES = T::BN * ROWB;
+  __device__ static __forceinline__ int swz(int r) { return (r >> 1) & 7; }  // slot of chunk c is c ^ swz(r)
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int LA = T::BM / 8 / WAVES;  // 1 KB loads per wave and k-tile
   static constexpr int LB = T::BN / 8 / WAVES;
@@ -744,6 +747,167 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
   finish_tile<T, EPI>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
 }
 
+// Affine-quantised W on the direct-load layout: A moves global -> LDS by
+// direct loads as in gemm_dl_kernel; W's codes (one 16-byte chunk per code
+// row and k-half or quarter), scales and biases come into registers one
+// k-tile ahead, and after the k-tile's MFMAs each thread dequantises its
+// chunk (w = scale * q + bias, rounded once to bf16, as in gemm_kernel) and
+// writes it into the next stage's B tile in the same swizzled layout, so the
+// fragment reads and the MFMA loop are gemm_dl_kernel's.  Only W passes
+// through ds_write (half of the register-staged kernel's LDS writes).
+template <class T, int AM, int BQ>
+__global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p) {
+  using L = DlLayout<T, 2>;
+  static_assert(BQ == 4 || BQ == 8, "4- or 8-bit codes");
+  extern __shared__ __attribute__((aligned(16))) uint16_t dyn_lds[];
+  char* lds = reinterpret_cast<char*>(dyn_lds);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave / T::WN, wn = wave % T::WN;
+  const int2 tc = tile_coords(p.xcd_band);
+  const int m0 = tc.y * T::BM, n0 = tc.x * T::BN;
+
+  const uint16_t* a_src[L::LA];
+#pragma unroll
+  for (int j = 0; j < L::LA; ++j) {
+    const int r = (wave * L::LA + j) * L::RPI + lane / L::CPR;
+    const int c = (lane % L::CPR) ^ L::swz(r);
+    a_src[j] = a_row_ptr<AM>(p, min(m0 + r, p.M - 1)) + 8 * c;
+  }
+  auto issue_a = [&](int kt, int stage) {
+    char* a_dst = lds + stage * L::STAGE + wave * L::LA * 1024;
+#pragma unroll
+    for (int j = 0; j < L::LA; ++j) load_lds16(a_src[j] + kt * T::BK, a_dst + j * 1024);
+  };
+
+  // W codes: a 16-byte chunk holds QVALS codes of one row; a row's k-tile (one
+  // quantisation group of 64) is QCH chunks; each thread owns CQ chunks.
+  constexpr int QVALS = 128 / BQ;
+  constexpr int QCH = T::BK / QVALS;
+  constexpr int CQ = T::BN * QCH / T::THREADS;
+  static_assert(CQ * T::THREADS == T::BN * QCH, "quantised tile loads must divide evenly");
+  const uint32_t* q_src[CQ];
+  const uint16_t* s_src[CQ];
+  const uint16_t* z_src[CQ];
+  int q_row[CQ], q_part[CQ];
+#pragma unroll
+  for (int c = 0; c < CQ; ++c) {
+    const int chunk = tid + c * T::THREADS;
+    const int row = chunk / QCH, part = chunk % QCH;
+    const int64_t n = min(n0 + row, p.N - 1);
+    q_row[c] = row;
+    q_part[c] = part;
+    q_src[c] = p.Wq + n * p.ldq + part * (QVALS * BQ / 32);
+    s_src[c] = p.qscale + n * (p.K / 64);
+    z_src[c] = p.qbias + n * (p.K / 64);
+  }
+  u32x4_t rq[CQ];
+  uint16_t rs[CQ], rz[CQ];
+  auto fetch_w = [&](int kt) {
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) {
+      rq[c] = *reinterpret_cast<const u32x4_t*>(q_src[c] + kt * T::BK * BQ / 32);
+      rs[c] = s_src[c][kt];
+      rz[c] = z_src[c][kt];
+    }
+  };
+  auto stash_w = [&](int stage) {
+    char* b_base = lds + stage * L::STAGE + L::A_BYTES;
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) {
+      const float sc = f16_to_f32(rs[c]), bi = f16_to_f32(rz[c]);
+      const int r = q_row[c];
+#pragma unroll
+      for (int o = 0; o < QVALS / 8; ++o) {  // 8 codes -> one 16-byte bf16 chunk
+        u32x4_t v;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int first = o * 8 + 2 * h;  // code index inside the chunk
+          const int word = first * BQ / 32, shift = (first * BQ) % 32;
+          v[h] = dq_pair<BQ>(rq[c][word], shift, sc, bi);
+        }
+        const int lc = q_part[c] * (QVALS / 8) + o;  // logical 16-byte chunk of the row
+        *reinterpret_cast<u32x4_t*>(b_base + r * L::ROWB + ((lc ^ L::swz(r)) * 16)) = v;
+      }
+    }
+  };
+
+  f32x16_t acc[T::TM][T::TN];
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int frag_row = lane & 31;
+  const int ysw = (lane >> 5) ^ L::swz(frag_row);
+  const int a_off = (wm * T::WTM + frag_row) * L::ROWB;
+  const int b_off = L::A_BYTES + (wn * T::WTN + frag_row) * L::ROWB;
+  constexpr int KS = T::BK / 16;
+  bf16x8_t af[2][T::TM], bfr[2][T::TN];
+  auto read_frags = [&](int stage, int ks, int slot) {
+    const int cofs = ((2 * ks) ^ ysw) * 16;
+    const char* a_l = lds + stage * L::STAGE + a_off + cofs;
+    const char* b_l = lds + stage * L::STAGE + b_off + cofs;
+    af[slot][0] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(a_l));
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+      bfr[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(b_l + 32 * j * L::ROWB));
+#pragma unroll
+    for (int i = 1; i < T::TM; ++i)
+      af[slot][i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(a_l + 32 * i * L::ROWB));
+  };
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+  };
+  auto interleave = [&]() {
+#pragma unroll
+    for (int r = 0; r < T::TM + T::TN; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, T::TM * T::TN - (T::TM + T::TN), 0);
+  };
+
+  // Two stages.  Tile kt+1's A is requested and its W codes fetched at the
+  // top of tile kt; W is dequantised into the other stage after the k-tile's
+  // reads of it are done (the previous barrier), before the barrier that ends
+  // tile kt, whose fence covers both the direct loads and the LDS writes.
+  const int kt_n = p.K / T::BK;
+  issue_a(0, 0);
+  fetch_w(0);
+  stash_w(0);
+  __syncthreads();
+  read_frags(0, 0, 0);
+  int stage = 0;
+  for (int kt = 0; kt < kt_n; ++kt) {
+    const bool more = kt + 1 < kt_n;
+    if (more) {
+      issue_a(kt + 1, stage ^ 1);
+      fetch_w(kt + 1);
+    }
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      read_frags(stage, ks + 1, (ks + 1) & 1);
+      mfma_step(ks & 1);
+      interleave();
+    }
+    if (more) stash_w(stage ^ 1);
+    __syncthreads();
+    if (more) read_frags(stage ^ 1, 0, 0);
+    mfma_step((KS - 1) & 1);
+    if (more) interleave();
+    stage ^= 1;
+  }
+  const RowMeta rm{0, 0};
+  finish_tile<T, kEpiStore>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm rows (HF LlamaRMSNorm): y = w * bf16(x * rsqrt(mean(x^2) + eps)).
 // With delta != nullptr: residual = bf16(residual + delta) first (the
@@ -844,6 +1008,26 @@ int launch_dl(const GemmParams& p, hipStream_t st) {
 }
 
 using TileD = Tile<256, 256, BK, 2, 4>;  // direct-load large tile
+
+template <class T, int AM, int BQ>
+int launch_dlq(const GemmParams& p, hipStream_t st) {
+  using L = DlLayout<T, 2>;
+  static bool lds_set[64] = {false};
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= 64 || !lds_set[dev]) {
+    if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dlq_kernel<T, AM, BQ>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS),
+                           "gemm_dlq_kernel LDS attribute"))
+      return rc;
+    if (dev >= 0 && dev < 64) lds_set[dev] = true;
+  }
+  const dim3 grid((p.N + T::BN - 1) / T::BN, (p.M + T::BM - 1) / T::BM), block(T::THREADS);
+  hipLaunchKernelGGL((gemm_dlq_kernel<T, AM, BQ>), grid, block, L::LDS, st, p);
+  YAPD_LAUNCH_CHECK("gemm_dlq_kernel launch");
+  return YAPD_OK;
+}
+
 using TileW = Tile<64, 64, BK, 1, 1>;     // direct-load one-wave tile (small batches)
 
 // Compute units of the current device (cached per device id).
@@ -868,8 +1052,12 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   const int64_t big_tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
   if (big_tiles >= (BQ == 0 ? cu_count() * 3 / 4 : 256)) {
     p.xcd_band = big_tiles <= cu_count() ? 1 : 0;
-    if constexpr (BQ == 0) return launch_dl<TileD, EPI, AM>(p, st);
-    return launch_tile<TileL, EPI, AM, BQ>(p, st);
+    if constexpr (BQ == 0) {
+      return launch_dl<TileD, EPI, AM>(p, st);
+    } else {
+      static_assert(EPI == kEpiStore, "the quantised path stores plainly");
+      return launch_dlq<TileD, AM, BQ>(p, st);
+    }
   }
   // Few tiles (small batches): one-wave 64 x 64 direct-load tiles with two
   // k-tiles in flight, while they give at most two workgroups per CU
