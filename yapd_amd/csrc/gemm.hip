@@ -5,10 +5,12 @@
 // v_mfma_f32_32x32x16_bf16.  Large M: `gemm_dl_kernel`, a 256 x 256 tile of
 // 8 waves (128 x 64 each) whose A and W k-slices go global -> LDS by direct
 // loads into two 64 KB stages.  Small M: the same kernel on one-wave 64 x 64
-// tiles with three stages.  Mid M and the quantised W path: `gemm_kernel`,
-// register-staged 128 x 128 (or 256 x 256) tiles with padded LDS rows.  Every
-// kernel runs the same MFMA over the same K order, so a row's result does not
-// depend on which kernel the batch size selects.  K advances in steps of 64.
+// tiles with three stages.  Mid M: `gemm_kernel`, register-staged 128 x 128
+// tiles with padded LDS rows.  Every kernel runs the same MFMA over the same K
+// order, so a row's result does not depend on which kernel the batch size
+// selects.  Affine-quantised W: `gemm_dlq_kernel` (the direct-load layout with
+// W dequantised from registers into LDS) at large M, `gemm_kernel` below.  K
+// advances in steps of 64.
 //
 // Epilogues (once per output element):
 //   * store    -- plain bf16 store (speech head, small projections);
@@ -976,7 +978,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const NormParams p) {
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 using TileS = Tile<128, 128, BK, 2, 2>;  // small M: more workgroups
-using TileL = Tile<256, 256, BK, 2, 4>;  // large M: 8 waves of 128 x 64
 
 template <class T, int EPI, int AM, int BQ>
 int launch_tile(const GemmParams& p, hipStream_t st) {
@@ -1050,7 +1051,7 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   // tiles the 128 x 128 kernel is still faster) or, for the quantised path,
   // once they give one workgroup per CU.
   const int64_t big_tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
-  if (big_tiles >= (BQ == 0 ? cu_count() * 3 / 4 : 256)) {
+  if (big_tiles >= (BQ == 0 ? cu_count() * 3 / 4 : cu_count())) {
     p.xcd_band = big_tiles <= cu_count() ? 1 : 0;
     if constexpr (BQ == 0) {
       return launch_dl<TileD, EPI, AM>(p, st);
