@@ -13,7 +13,9 @@ scoring, replayed as one HIP graph.
 Prints one JSON line.  ``value`` = speech tokens/s = pairs * block / step time.
 ``roofline`` describes the dominant kernel (the gate/up + SiLU GEMM) against
 the published bf16 peak and, as ``peak_measured``, against the sustained MFMA
-rate of a register-only calibration kernel; ``kernels`` adds attention and
+rate of a register-only calibration kernel on random operands spread like the
+step's (``peak_measured_constant_operands``: the same kernel on few-bit
+constants, which draw less power and run faster); ``kernels`` adds attention and
 scoring against the HBM roofline.  Per-kernel durations come from HIP events
 on the stream the kernel runs on, right after the timed region: around single
 launches for the GEMMs, and around one graph replay of 20 back-to-back calls
@@ -217,6 +219,7 @@ def main():
                            20, dev)
 
     peak_meas = measured_mfma_peak(dev)
+    peak_meas_const = measured_mfma_peak(dev, random_operands=False)
     csrc = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
     cdst = torch.empty_like(csrc)
     ms_copy = time_launches(lambda: cdst.copy_(csrc), 10, dev)
@@ -269,7 +272,8 @@ def main():
         "roofline": {"kernel": "gemm_dl_kernel<swiglu> (gate/up + SiLU*up, M=%d N=%d K=%d)" % (N, 2 * F, D),
                      "bound": "mfma", "achieved": round(tf_swiglu, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf_swiglu / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
-                     "peak_measured": round(peak_meas, 1), "frac_of_measured": round(tf_swiglu / peak_meas, 4)},
+                     "peak_measured": round(peak_meas, 1), "frac_of_measured": round(tf_swiglu / peak_meas, 4),
+                     "peak_measured_constant_operands": round(peak_meas_const, 1)},
         "kernels": {
             "attention": {"us": round(ms_attn * 1e3, 1), "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4)},
@@ -287,14 +291,15 @@ def main():
 COPY_BYTES = 1 << 30
 
 
-def measured_mfma_peak(dev):
+def measured_mfma_peak(dev, random_operands=True):
     """Sustained bf16 MFMA TFLOP/s of the register-only calibration kernel
-    (8 waves per SIMD, 2000 rounds of 8 independent 32x32x16 MFMAs)."""
+    (8 waves per SIMD, 2000 rounds of 8 independent 32x32x16 MFMAs) on random
+    operands spread like the step's (the default) or on few-bit constants."""
     from yapd_amd import kernels
     blocks, iters = 2048, 2000
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
-    flops = kernels.mfma_peak_probe(blocks, iters, out)
-    ms = time_launches(lambda: kernels.mfma_peak_probe(blocks, iters, out), 5, dev)
+    flops = kernels.mfma_peak_probe(blocks, iters, out, random_operands)
+    ms = time_launches(lambda: kernels.mfma_peak_probe(blocks, iters, out, random_operands), 5, dev)
     return flops / (ms * 1e-3) / 1e12
 
 

@@ -3,9 +3,11 @@
  *
  * yapd_mfma_peak_probe: `blocks` workgroups of 4 waves each run `iters`
  * rounds of 8 independent v_mfma_f32_32x32x16_bf16 on register operands and
- * store one float per thread to out[blocks * 256].  Work per call:
- * blocks * 4 * iters * 8 * 32768 flops; the sustained bf16 MFMA rate is that
- * divided by the launch time. */
+ * store one float per thread to out[blocks * 256].  random_operands != 0: each
+ * accumulator's operand pair holds random bf16 spread like activations (unit
+ * scale) and weights (scale 0.02); 0: the same few-bit constants for all.
+ * Work per call: blocks * 4 * iters * 8 * 32768 flops; the sustained bf16
+ * MFMA rate is that divided by the launch time. */
 #ifndef YAPD_PROBE_H
 #define YAPD_PROBE_H
 
@@ -13,7 +15,7 @@
 extern "C" {
 #endif
 
-int yapd_mfma_peak_probe(int blocks, int iters, float* out, void* stream);
+int yapd_mfma_peak_probe(int blocks, int iters, int random_operands, float* out, void* stream);
 
 #ifdef __cplusplus
 }

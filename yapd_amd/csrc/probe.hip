@@ -1,5 +1,7 @@
-// Sustained bf16 MFMA rate on register operands (the measured denominator the
-// harness reports next to the published 2.5 PFLOP/s).
+// Sustained bf16 MFMA rate on register operands (the measured denominators the
+// harness reports next to the published 2.5 PFLOP/s).  The rate depends on the
+// operand values: random operands draw more power than few-bit constants and
+// the part sustains ~20 % less with them.
 #include "common.h"
 #include "../../include/yapd_probe.h"
 
@@ -8,13 +10,35 @@ namespace {
 
 constexpr int kProbeAcc = 8;
 
+__device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// Eight independent accumulators, each with its own operand pair.  RANDOM:
+// the pairs hold random bf16 spread like the step's operands (activations of
+// unit scale, weights of scale 0.02), so consecutive MFMAs switch between
+// unrelated values; otherwise all eight pairs are the same few-bit constants.
+template <bool RANDOM>
 __global__ __launch_bounds__(256) void mfma_peak_kernel(float* out, int iters) {
-  bf16x8_t a, b;
+  bf16x8_t a[kProbeAcc], b[kProbeAcc];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = static_cast<__bf16>(static_cast<float>(threadIdx.x & 7) * 0.125f + static_cast<float>(i));
-    b[i] = static_cast<__bf16>(static_cast<float>(i) * 0.5f - 1.f);
-  }
+  for (int j = 0; j < kProbeAcc; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (RANDOM) {
+        const uint32_t h = probe_hash(threadIdx.x * 131u + j * 17u + i * 7919u + blockIdx.x * 104729u);
+        a[j][i] = static_cast<__bf16>((static_cast<float>(h & 0xffffu) * 0x1p-16f - 0.5f) * 3.4f);
+        b[j][i] = static_cast<__bf16>((static_cast<float>(h >> 16) * 0x1p-16f - 0.5f) * 0.07f);
+      } else {
+        a[j][i] = static_cast<__bf16>(static_cast<float>(threadIdx.x & 7) * 0.125f + static_cast<float>(i));
+        b[j][i] = static_cast<__bf16>(static_cast<float>(i) * 0.5f - 1.f);
+      }
+    }
   f32x16_t acc[kProbeAcc];
 #pragma unroll
   for (int j = 0; j < kProbeAcc; ++j)
@@ -22,7 +46,7 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(float* out, int iters) {
     for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
-    for (int j = 0; j < kProbeAcc; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+    for (int j = 0; j < kProbeAcc; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], b[j], acc[j], 0, 0, 0);
   }
   float s = 0.f;
 #pragma unroll
@@ -35,10 +59,14 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(float* out, int iters) {
 }  // namespace
 }  // namespace yapd
 
-extern "C" int yapd_mfma_peak_probe(int blocks, int iters, float* out, void* stream) {
+extern "C" int yapd_mfma_peak_probe(int blocks, int iters, int random_operands, float* out, void* stream) {
   YAPD_REQUIRE(out != nullptr && blocks >= 1 && blocks <= (1 << 20) && iters >= 1,
                "mfma_peak_probe: need out and 1 <= blocks <= 2^20, iters >= 1");
-  hipLaunchKernelGGL(yapd::mfma_peak_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), out, iters);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (random_operands)
+    hipLaunchKernelGGL(yapd::mfma_peak_kernel<true>, dim3(blocks), dim3(256), 0, st, out, iters);
+  else
+    hipLaunchKernelGGL(yapd::mfma_peak_kernel<false>, dim3(blocks), dim3(256), 0, st, out, iters);
   YAPD_LAUNCH_CHECK("mfma_peak_kernel launch");
   return YAPD_OK;
 }

@@ -49,7 +49,7 @@ _SIGNATURES = {
     "yapd_rmsnorm": (c_int, [c_void, c_void, c_void, c_void, c_float, c_int, c_int, c_void, c_void]),
     "yapd_qgemm_affine": (c_int, [c_void, c_i64, c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_int,
                                   c_void, c_i64, c_void]),
-    "yapd_mfma_peak_probe": (c_int, [c_int, c_int, c_void, c_void]),
+    "yapd_mfma_peak_probe": (c_int, [c_int, c_int, c_int, c_void, c_void]),
     "yapd_tick_update": (c_int, [c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_void, c_i64,
                                  c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void,
                                  c_void, c_void]),
@@ -421,11 +421,13 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor,
                                       out.data_ptr(), stream_ptr(dev)))
 
 
-def mfma_peak_probe(blocks: int, iters: int, out: torch.Tensor) -> float:
-    """Launch the register-only MFMA calibration kernel; returns its flop count."""
+def mfma_peak_probe(blocks: int, iters: int, out: torch.Tensor, random_operands: bool = True) -> float:
+    """Launch the register-only MFMA calibration kernel (random or constant operands); returns its
+    flop count."""
     require_cuda(out, "out", torch.float32, out.device)
     require(out.numel() >= blocks * 256, "out needs blocks * 256 floats")
-    check(load_library().yapd_mfma_peak_probe(blocks, iters, out.data_ptr(), stream_ptr(out.device)))
+    check(load_library().yapd_mfma_peak_probe(blocks, iters, int(bool(random_operands)), out.data_ptr(),
+                                              stream_ptr(out.device)))
     return float(blocks) * 4 * iters * 8 * 32768
 
 
