@@ -121,9 +121,43 @@ __device__ __forceinline__ RowMeta qkv_row_meta(const GemmParams& p, int m0, int
   return rm;
 }
 
+// Columns 0..31 of the cos and sin rows at every tile row's position, copied
+// to LDS by the whole workgroup with one round trip to memory: the epilogue
+// then reads LDS, whose waits (lgkmcnt) do not cover its own global stores,
+// instead of a load and a store acknowledgement per 4-dim run.  Layout: a
+// [BM][kRopePitch] cos block, then the sin block; the 36-float pitch puts the
+// 16-byte reads of 8 consecutive rows in distinct banks.
+constexpr int kRopePitch = 36;
+
+template <class T>
+constexpr int qkv_lds_bytes() {
+  return T::BM * static_cast<int>(sizeof(RowMeta)) + 2 * T::BM * kRopePitch * 4;
+}
+
+template <class T>
+__device__ __forceinline__ void stage_rope_rows(const GemmParams& p, const RowMeta* meta, float* rope, int tid) {
+  constexpr int kChunks = T::BM * 16;  // per row: 8 x 16 bytes of cos, 8 of sin
+  static_assert(kChunks % T::THREADS == 0, "whole chunks per thread");
+  constexpr int kPer = kChunks / T::THREADS;
+  f32x4_t v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int c = tid + j * T::THREADS;
+    const int row = c >> 4, part = c & 15;
+    const int pc = min(max(meta[row].pos, 0), p.max_pos - 1);
+    v[j] = *reinterpret_cast<const f32x4_t*>((part < 8 ? p.cos_t : p.sin_t) + pc * kHeadDim + 4 * (part & 7));
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int c = tid + j * T::THREADS;
+    const int row = c >> 4, part = c & 15;
+    *reinterpret_cast<f32x4_t*>(rope + ((part >> 3) * T::BM + row) * kRopePitch + 4 * (part & 7)) = v[j];
+  }
+}
+
 // qkv epilogue: NeoX RoPE on q and k from the cos/sin tables at each row's
 // position; the tables are HF's cat(freqs, freqs) layout, so column d + 32
-// equals column d and only columns 0..31 are read.  The qkv GEMM multiplies
+// equals column d and only columns 0..31 are read (staged in `rope`).  The qkv GEMM multiplies
 // W x A^T (MFMA operands swapped), so lane l holds token (l & 31) of each
 // 32-row block and, in each 32-column block, head dims
 // 8 * (e / 4) + 4 * (l / 32) + e % 4 for accumulator element e: four runs of
@@ -132,10 +166,11 @@ __device__ __forceinline__ RowMeta qkv_row_meta(const GemmParams& p, int m0, int
 // 64 and 64 divides n_heads * 64).  So a lane does RoPE on whole runs
 // (16-byte cos/sin loads), stores q and k as 8-byte runs, and a V column
 // (layout d * 16 + slot) is written by 32 lanes with consecutive slots.
-// `meta` holds the RowMeta of the tile rows.
+// `meta` holds the RowMeta of the tile rows, `rope` their cos/sin columns.
 template <class T, int SECTION>
 __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
-                                                     const RowMeta* meta, int m0, int nb, int q2, int wm, int lane) {
+                                                     const RowMeta* meta, const float* rope, int m0, int nb, int q2,
+                                                     int wm, int lane) {
   const int tok = lane & 31;
   const int dgrp = 4 * (lane >> 5);
   const int HD = p.n_heads * kHeadDim;
@@ -146,7 +181,6 @@ __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const 
     const int m = m0 + rl;
     if (m >= p.M) continue;
     const RowMeta mt = meta[rl];
-    const int pc = min(max(mt.pos, 0), p.max_pos - 1);
     const int slot = mt.pos & (kPageSize - 1);
     uint16_t* const kv = p.pool + kv_plane_offset(mt.page, SECTION == 2 ? 1 : 0, head, p.n_heads);
 #pragma unroll
@@ -161,8 +195,8 @@ __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const 
         X1[h] = pack_bf16x2(acc[i][2 * q2 + 1][4 * r4 + 2 * h], acc[i][2 * q2 + 1][4 * r4 + 2 * h + 1]);
       }
       if constexpr (SECTION < 2) {
-        const f32x4_t c = *reinterpret_cast<const f32x4_t*>(p.cos_t + pc * kHeadDim + d0);
-        const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(p.sin_t + pc * kHeadDim + d0);
+        const f32x4_t c = *reinterpret_cast<const f32x4_t*>(rope + rl * kRopePitch + d0);
+        const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(rope + (T::BM + rl) * kRopePitch + d0);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           // x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1], each op rounded
@@ -198,18 +232,19 @@ __device__ __forceinline__ void epilogue_qkv_section(const GemmParams& p, const 
 
 template <class T>
 __device__ __forceinline__ void epilogue_qkv(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN],
-                                             const RowMeta* meta, int m0, int n_base, int wm, int lane) {
+                                             const RowMeta* meta, const float* rope, int m0, int n_base, int wm,
+                                             int lane) {
   const int HD = p.n_heads * kHeadDim;
 #pragma unroll
   for (int q2 = 0; q2 < T::TN / 2; ++q2) {
     const int nb = n_base + 64 * q2;
     const int section = nb / HD;  // 0 q, 1 k, 2 v
     if (section == 0) {
-      epilogue_qkv_section<T, 0>(p, acc, meta, m0, nb, q2, wm, lane);
+      epilogue_qkv_section<T, 0>(p, acc, meta, rope, m0, nb, q2, wm, lane);
     } else if (section == 1) {
-      epilogue_qkv_section<T, 1>(p, acc, meta, m0, nb, q2, wm, lane);
+      epilogue_qkv_section<T, 1>(p, acc, meta, rope, m0, nb, q2, wm, lane);
     } else {
-      epilogue_qkv_section<T, 2>(p, acc, meta, m0, nb, q2, wm, lane);
+      epilogue_qkv_section<T, 2>(p, acc, meta, rope, m0, nb, q2, wm, lane);
     }
   }
 }
@@ -369,7 +404,7 @@ __device__ __forceinline__ int2 tile_coords(int xcd_band) {
 
 // Epilogue dispatch.  Every wave has finished reading the LDS stages (the
 // main loop ends with a barrier and no LDS reads after it), so the epilogues
-// may reuse all of LDS.
+// may reuse all of LDS (at least qkv_lds_bytes<T>() of it for kEpiQkv).
 template <class T, int EPI>
 __device__ __forceinline__ void finish_tile(const GemmParams& p, const f32x16_t (&acc)[T::TM][T::TN], uint16_t* lds,
                                             const RowMeta& rm, int m0, int n0, int wm, int wn, int lane, int tid) {
@@ -381,9 +416,14 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, const f32x16_t 
     epilogue_swiglu<T>(p, acc, m0, n0, wm, wn, lane);
   } else {
     RowMeta* meta = reinterpret_cast<RowMeta*>(lds);
+    float* rope = reinterpret_cast<float*>(meta + T::BM);
     if (tid < T::BM) meta[tid] = rm;
     __syncthreads();
-    epilogue_qkv<T>(p, acc, meta, m0, n0 + wn * T::WTN, wm, lane);
+    if (n0 < 2 * p.n_heads * kHeadDim) {  // q or k columns in this tile (uniform per workgroup)
+      stage_rope_rows<T>(p, meta, rope, tid);
+      __syncthreads();
+    }
+    epilogue_qkv<T>(p, acc, meta, rope, m0, n0 + wn * T::WTN, wm, lane);
   }
 }
 
@@ -554,6 +594,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_kernel(const GemmParams p) {
     mfma_step((KS - 1) & 1);
     if (more) interleave();
   }
+  static_assert(EPI != kEpiQkv || qkv_lds_bytes<T>() <= static_cast<int>(sizeof(smem)), "qkv epilogue LDS");
   finish_tile<T, EPI>(p, acc, smem, rm, m0, n0, wm, wn, lane, tid);
 }
 
@@ -746,6 +787,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
     if (more) interleave();
     stage = next;
   }
+  static_assert(EPI != kEpiQkv || qkv_lds_bytes<T>() <= L::LDS, "qkv epilogue LDS");
   finish_tile<T, EPI>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
 }
 
