@@ -54,3 +54,102 @@ def test_score_rejects_bad_arguments_without_launch():
     assert rc == 1 and b"bl" in lib.yapd_last_error()
     with pytest.raises(ValueError):
         kernels.check(1)
+
+
+# Device pointers are never dereferenced by the host-side checks, so a fake
+# 16-byte-aligned address stands in for them; a rejected call returns
+# YAPD_EINVAL before any HIP call, which is why these run without a GPU.
+P = 4096
+EINVAL = 1
+GEMM = (P, 1024, P, 1024)
+REJECTS = [
+    ("yapd_gemm_bf16", (*GEMM, 0, 1024, 1024, P, 1024, None), b"need M, N >= 1"),
+    ("yapd_gemm_bf16", (*GEMM, 64, 1024, 100, P, 1024, None), b"K=100"),
+    ("yapd_gemm_bf16", (P + 2, 1024, P, 1024, 64, 1024, 1024, P, 1024, None), b"A must be 16-byte aligned"),
+    ("yapd_gemm_bf16", (*GEMM, 64, 1024, 1024, P, 512, None), b"bad C"),
+    ("yapd_gemm_bf16_residual", (*GEMM, 64, 1024, 1024, None, 1024, None), b"bad residual"),
+    ("yapd_gemm_swiglu", (P, 1024, P, 64, 100, 1024, P, 100, None), b"F must be a multiple of 64"),
+    ("yapd_gemm_head_shift", (P, None, 4, 32, 1024, P, 1024, 8194, P, 8200, None), b"bad shift_ctx"),
+    ("yapd_gemm_qkv_rope_kv", (P, 1024, P, 48, 1024, 16, P, P, 2048, P, 32, P, P, 64, P, 8, 8, None),
+     b"bad positions / table shape"),
+    ("yapd_gemm_qkv_rope_kv", (P, 1024, P, 64, 1024, 16, P + 4, P, 2048, P, 32, P, P, 64, P, 8, 8, None),
+     b"cos/sin must be 16-byte aligned"),
+    ("yapd_rmsnorm", (None, None, P, P, 1e-5, 64, 1000, P, None), b"D must be a multiple of 512"),
+    ("yapd_rmsnorm", (P, P, P, P, 1e-5, 64, 1024, P, None), b"not both"),
+    ("yapd_rmsnorm", (None, None, P, P, 1e-5, 0, 1024, P, None), b"empty"),
+    ("yapd_qgemm_affine", (P, 1024, P, P, P, 3, 64, 64, 1024, 1024, P, 1024, None), b"bits must be 4 or 8"),
+    ("yapd_qgemm_affine", (P, 1024, P, P, P, 4, 32, 64, 1024, 1024, P, 1024, None), b"group_size must be 64"),
+    ("yapd_attn_paged_block", (P, P, 64, P, 8, 8, P, 4, 65, 16, P, 4, None, 0, None, None, None, 0, 0.125, 0, P,
+                               None), b"1 <= bl <= 64"),
+    ("yapd_attn_paged_block", (P, P, 64, P, 8, 8, P, 4, 32, 6, P, 4, None, 0, None, None, None, 0, 0.125, 0, P,
+                               None), b"n_heads must be a multiple of 4"),
+    ("yapd_attn_paged_block", (P, P, 64, P, 8, 8, P, 4, 32, 16, P, 4, P, 2, None, None, None, 0, 0.125, 0, P,
+                               None), b"split items need a workspace"),
+    ("yapd_kv_write", (P, P, 1028, 1028, P, 64, P, 8, 8, P, 4, 32, 16, None), b"multiples of 8"),
+    ("yapd_kv_write", (P, P, 1024, 1024, P, 64, P, 8, 8, P, 0, 32, 16, None), b"empty shape"),
+    ("yapd_kv_gather", (P, 64, None, 8, 100, 16, P, P, None), b"NULL pointer"),
+    ("yapd_tick_update", (4, 16, 3, 1024, 10, 8194, 6562, 4096, 2048, P, 2048, P, P, P, P, P, P, P, P, P, P, P,
+                          None), b"bad sizes"),
+    ("yapd_tick_update", (4, 16, 2, 1024, 10, 8194, 6562, 16, 2048, P, 2048, P, P, P, P, P, P, P, P, P, P, P,
+                          None), b"bad max_len"),
+    ("yapd_snake", (P, P, None, P, 2, 64, 0, None), b"need B, C, T >= 1"),
+    ("yapd_residual_bias", (P, None, P, P, 2, 64, 100, None), b"NULL residual"),
+    ("yapd_mean3", (P, P, P, P, 0, None), b"n must be >= 1"),
+    ("yapd_residual_bias_snake", (P, P, P, None, P, P, 2, 64, 100, None), b"NULL pointer"),
+    ("yapd_branch_start", (P, P, P, P, P, P, P, None, P, 2, 64, 100, None), b"NULL pointer"),
+    ("yapd_mfma_peak_probe", (0, 10, 1, P, None), b"1 <= blocks"),
+]
+
+
+@pytest.mark.parametrize("name,args,msg", REJECTS, ids=[f"{r[0]}-{i}" for i, r in enumerate(REJECTS)])
+def test_entry_points_reject_bad_arguments_without_launch(name, args, msg):
+    lib = kernels.load_library()
+    assert getattr(lib, name)(*args) == EINVAL
+    assert msg in lib.yapd_last_error(), lib.yapd_last_error()
+
+
+def test_tick_update_with_no_slots_is_a_no_op():
+    lib = kernels.load_library()
+    assert lib.yapd_tick_update(0, 16, 2, 1024, 10, 8194, 6562, 4096, 2048, None, 2048, *([None] * 11), None) == 0
+
+
+def _block_forward_args(**model_overrides):
+    layer = kernels.T3Layer(P, P, P, P, P, P, 1e-5, 1e-5, P)
+    layers = (kernels.T3Layer * 2)(layer, layer)
+    fields = dict(n_layers=2, hidden=1024, n_heads=16, ffn=4096, layers=layers, final_norm=P, final_eps=1e-5,
+                  rope_cos=P, rope_sin=P, rope_positions=2048, n_pages=64, page_table=P, table_stride=8,
+                  table_cols=8)
+    fields.update(model_overrides)
+    model = kernels.T3Model(**fields)
+    ws = kernels.T3Workspace(P, P, P, P, P, P, P, 4, None, 0, None, None, None, 0)
+    return model, ws, layers
+
+
+@pytest.mark.parametrize("override,msg", [
+    (dict(n_heads=6), b"n_heads must be a multiple of 4"),
+    (dict(ffn=100), b"ffn must be a multiple of 64"),
+    (dict(hidden=1000), b"hidden must be"),
+    (dict(rope_cos=None), b"missing RoPE tables"),
+    (dict(table_stride=4), b"bad page table"),
+])
+def test_block_forward_checks_every_layer_rule_before_launching(override, msg):
+    """A shape that only a later per-layer call would reject is refused before
+    the first launch, so nothing (residual, KV pools, outputs) is modified."""
+    lib = kernels.load_library()
+    model, ws, _keep = _block_forward_args(**override)
+    rc = lib.yapd_t3_block_forward(ctypes.byref(model), ctypes.byref(ws), P, 4, 32, P, P, 0, P, None, 0, None,
+                                   None, 0, None)
+    assert rc == EINVAL and msg in lib.yapd_last_error(), lib.yapd_last_error()
+
+
+def test_block_forward_rejects_incomplete_layer_and_head():
+    lib = kernels.load_library()
+    model, ws, layers = _block_forward_args()
+    layers[1].w_down = None
+    rc = lib.yapd_t3_block_forward(ctypes.byref(model), ctypes.byref(ws), P, 4, 32, P, P, 0, P, None, 0, None,
+                                   None, 0, None)
+    assert rc == EINVAL and b"layer 1 has a NULL weight" in lib.yapd_last_error()
+    model, ws, _keep = _block_forward_args()
+    rc = lib.yapd_t3_block_forward(ctypes.byref(model), ctypes.byref(ws), P, 4, 32, P, P, 0, P, P, 8194, P,
+                                   P, 8000, None)
+    assert rc == EINVAL and b"ld_logits >= vocab" in lib.yapd_last_error()

@@ -27,6 +27,27 @@ extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_works
                "t3_block_forward: incomplete workspace");
   const int D = m->hidden, H = m->n_heads, F = m->ffn, HD = H * 64;
   const int M = rows * bl;
+  // The shape rules of every per-layer call, checked before the first launch,
+  // so that a rejected call leaves the residual, the KV pools and the outputs
+  // untouched (the calls below check them again).
+  YAPD_REQUIRE(D % 512 == 0 && D >= 512 && D <= 2048, "t3_block_forward: hidden must be 512, 1024, 1536 or 2048 (got %d)",
+               D);
+  // attention covers 4 heads per workgroup
+  YAPD_REQUIRE(H % 4 == 0 && H >= 4, "t3_block_forward: n_heads must be a multiple of 4 (got %d)", H);
+  YAPD_REQUIRE(F % 64 == 0 && F >= 64, "t3_block_forward: ffn must be a multiple of 64 (got %d)", F);
+  YAPD_REQUIRE(m->rope_cos && m->rope_sin && m->rope_positions >= 1 && m->final_norm,
+               "t3_block_forward: missing RoPE tables or final norm");
+  YAPD_REQUIRE(m->page_table && m->n_pages >= 1 && m->table_cols >= 1 && m->table_stride >= m->table_cols,
+               "t3_block_forward: bad page table");
+  for (int li = 0; li < m->n_layers; ++li) {
+    const yapd_t3_layer& L = m->layers[li];
+    YAPD_REQUIRE(L.w_qkv && L.w_o && L.w_gate_up && L.w_down && L.ln_in && L.ln_post && L.kv_pool,
+                 "t3_block_forward: layer %d has a NULL weight or KV pool", li);
+  }
+  YAPD_REQUIRE(ws->n_work >= 1 && (ws->n_merge == 0 || (ws->merge && ws->part_o && ws->part_ml && ws->n_slots >= 1)),
+               "t3_block_forward: bad attention plan in the workspace");
+  YAPD_REQUIRE(!head_w || (shift_ctx && logits && vocab >= 1 && ld_logits >= vocab),
+               "t3_block_forward: head needs shift_ctx, logits, vocab >= 1 and ld_logits >= vocab");
   const float scale = 0.125f;  // head_dim ** -0.5 for head_dim 64
   void* st = stream;
   auto* res = ws->residual;
@@ -50,7 +71,6 @@ extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_works
     YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, wn, eps, M, D, last ? hidden_out : xn, st));
   }
   if (head_w != nullptr) {
-    YAPD_REQUIRE(shift_ctx && logits && vocab >= 1, "t3_block_forward: head needs shift_ctx and logits");
     YAPD_TRY(yapd_gemm_head_shift(hidden_out, shift_ctx, rows, bl, D, head_w, D, vocab, logits, ld_logits, st));
   }
   return YAPD_OK;
