@@ -78,7 +78,7 @@ def test_gemm_swiglu(dev, M, K):
     assert rel_err(act.cpu(), ref.float()) <= 1.5e-2
 
 
-@pytest.mark.parametrize("rows", [6, 70])  # 70 x 32 rows: large-tile path
+@pytest.mark.parametrize("rows", [6, 70, 64])  # 70 x 32 rows: large tiles; 64 x 32: the 2 last columns split off
 def test_gemm_head_shift(dev, rows):
     bl, D, V = 32, 1024, 8194
     hidden = rnd(rows, bl, D, seed=8)
@@ -197,3 +197,23 @@ def test_rows_do_not_depend_on_batch_size(dev, epi):
     for r in res[1:]:
         assert torch.equal(res[0][0], r[0])
         assert torch.equal(res[0][1], r[1])
+
+
+def test_narrow_last_column_tile_is_split_bit_identically(dev):
+    """N = 32 x 256 + 2 (the speech head): when the 2-column tile would add a
+    round of 256 x 256 tiles, those columns run as a second launch on 64 x 64
+    tiles.  Rows must equal those of a small call (one launch on 64 x 64
+    tiles) bit for bit, and the tail columns must match the fp32 product."""
+    D, N = 1024, 8194
+    A = rnd(16384, D, seed=41).to(dev)
+    W = rnd(N, D, std=0.02, seed=42).to(dev)
+    outs = []
+    for M in (16384, 2048, 96):  # 2112 -> 9 rounds, 264 -> 2 rounds: split; 96 rows: one small launch
+        C = torch.empty(M, 8200, dtype=torch.bfloat16, device=dev)[:, :N]
+        kernels.gemm_bf16(A[:M], W, C)
+        outs.append(C.cpu())
+    assert torch.equal(outs[0][:96], outs[2])
+    assert torch.equal(outs[1][:96], outs[2])
+    assert torch.equal(outs[0][:2048], outs[1])
+    ref = A[:2048].cpu().float() @ W[-2:].cpu().float().T
+    assert rel_err(outs[1][:, -2:], ref) <= 8e-3

@@ -1096,6 +1096,26 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   if (big_tiles >= (BQ == 0 ? cu_count() * 3 / 4 : cu_count())) {
     p.xcd_band = big_tiles <= cu_count() ? 1 : 0;
     if constexpr (BQ == 0) {
+      if constexpr (EPI == kEpiStore) {
+        // A last column tile of at most 64 columns that would add a round of
+        // 256 x 256 tiles (the speech head: N = 8194 = 32 x 256 + 2, 2112
+        // tiles) goes to a second launch on one-wave 64 x 64 tiles.  Every
+        // element keeps the same MFMA and K order, so the output is the same.
+        const int64_t row_tiles = (p.M + 255) / 256, cols = p.N / 256, cus = cu_count();
+        const int tail = p.N % 256;
+        if (cols >= 1 && tail != 0 && tail <= 64 &&
+            (row_tiles * (cols + 1) + cus - 1) / cus > (row_tiles * cols + cus - 1) / cus) {
+          GemmParams rest = p;
+          p.N = static_cast<int>(cols * 256);
+          p.xcd_band = row_tiles * cols <= cus ? 1 : 0;
+          rest.W = p.W + static_cast<int64_t>(p.N) * p.ldw;
+          rest.C = p.C + p.N;
+          rest.N = tail;
+          rest.xcd_band = (p.M + 63) / 64 <= cus ? 1 : 0;
+          if (int rc = launch_dl<TileD, EPI, AM>(p, st)) return rc;
+          return launch_dl<TileW, EPI, AM, 3>(rest, st);
+        }
+      }
       return launch_dl<TileD, EPI, AM>(p, st);
     } else {
       static_assert(EPI == kEpiStore, "the quantised path stores plainly");
