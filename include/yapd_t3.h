@@ -223,7 +223,10 @@ typedef struct yapd_t3_workspace {
  * first position, kv_len [rows] (device) = pos0 + bl.  hidden_out [rows*bl,
  * D] receives the final-normed hidden.  If head_w != NULL the logits [rows,
  * bl, vocab] (row pitch ld_logits) are computed from hidden and shift_ctx
- * [rows, D]. */
+ * [rows, D].  The shape rules of every per-layer call (D a multiple of 512
+ * up to 2048, H a multiple of 4, F a multiple of 64, complete layers, tables,
+ * attention plan and head arguments) are checked before the first launch: on
+ * YAPD_EINVAL nothing has been launched. */
 int yapd_t3_block_forward(const yapd_t3_model* model, const yapd_t3_workspace* ws, const void* block_emb,
                           int rows, int bl, const int32_t* pos0, const int32_t* kv_len, int causal,
                           void* hidden_out, const void* head_w, int vocab, const void* shift_ctx, void* logits,
