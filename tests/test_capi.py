@@ -98,6 +98,8 @@ REJECTS = [
     ("yapd_residual_bias_snake", (P, P, P, None, P, P, 2, 64, 100, None), b"NULL pointer"),
     ("yapd_branch_start", (P, P, P, P, P, P, P, None, P, 2, 64, 100, None), b"NULL pointer"),
     ("yapd_mfma_peak_probe", (0, 10, 1, P, None), b"1 <= blocks"),
+    ("yapd_hbm_read_probe", (P, 100, 8, P, None), b"multiple of 16"),
+    ("yapd_hbm_read_probe", (P + 4, 1024, 8, P, None), b"16-byte aligned"),
 ]
 
 

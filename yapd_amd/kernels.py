@@ -50,6 +50,7 @@ _SIGNATURES = {
     "yapd_qgemm_affine": (c_int, [c_void, c_i64, c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_int,
                                   c_void, c_i64, c_void]),
     "yapd_mfma_peak_probe": (c_int, [c_int, c_int, c_int, c_void, c_void]),
+    "yapd_hbm_read_probe": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
     "yapd_tick_update": (c_int, [c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_void, c_i64,
                                  c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void,
                                  c_void, c_void]),
@@ -429,6 +430,21 @@ def mfma_peak_probe(blocks: int, iters: int, out: torch.Tensor, random_operands:
     check(load_library().yapd_mfma_peak_probe(blocks, iters, int(bool(random_operands)), out.data_ptr(),
                                               stream_ptr(out.device)))
     return float(blocks) * 4 * iters * 8 * 32768
+
+
+def hbm_read_probe(src: torch.Tensor, blocks: int, out: torch.Tensor) -> int:
+    """Launch the streaming-read calibration kernel over all of ``src`` (contiguous, 16-byte aligned,
+    a multiple of 16 bytes): workgroup b folds its contiguous share of 16-byte words, thread t of it the
+    words b P + t, b P + t + 256, ... (P = the share rounded up to 256 words) by XOR into ``out[b * 256 + t]``.
+    Returns the bytes read."""
+    dev = src.device
+    require(src.is_cuda and src.is_contiguous(), "src must be a contiguous GPU tensor")
+    nbytes = src.numel() * src.element_size()
+    require(nbytes % 16 == 0 and src.data_ptr() % 16 == 0, "src must be 16-byte aligned, a multiple of 16 bytes")
+    require_cuda(out, "out", torch.int32, dev)
+    require(out.numel() >= blocks * 256, "out needs blocks * 256 words")
+    check(load_library().yapd_hbm_read_probe(src.data_ptr(), nbytes, blocks, out.data_ptr(), stream_ptr(dev)))
+    return nbytes
 
 
 def tick_update(*, xt: torch.Tensor, xt_blk: torch.Tensor, xt_new: torch.Tensor, k_step: torch.Tensor,
