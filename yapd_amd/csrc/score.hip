@@ -209,11 +209,12 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
 
   const int n_pass = nw / kPass;
   uint32_t xc[kUnroll], xu[kUnroll];
+  // Each logit is read once: non-temporal loads (they stream past the caches).
   auto load_pass = [&](int base) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      xc[u] = wc[base + u * 64 + lane];
-      if (kHasU) xu[u] = wu[base + u * 64 + lane];
+      xc[u] = __builtin_nontemporal_load(wc + base + u * 64 + lane);
+      if (kHasU) xu[u] = __builtin_nontemporal_load(wu + base + u * 64 + lane);
     }
   };
   for (int pi = 0; pi < n_pass; ++pi) {
