@@ -110,14 +110,23 @@ __global__ __launch_bounds__(kVThreads) void voc_kernel(const VocParams p) {
     }
     if (threadIdx.x < v0 - g0) one(g0 + threadIdx.x);
     if (threadIdx.x < g1 - v1) one(v1 + threadIdx.x);
+    // Inputs are read once.  With one output, non-temporal loads (past the
+    // caches) measured 12-19 % faster; with two or four outputs 4-5 % slower.
+    auto load = [](const float* src) {
+      if constexpr (kOut == 1) {
+        return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(src));
+      } else {
+        return *reinterpret_cast<const f32x4_t*>(src);
+      }
+    };
     f32x4_t xv[kVecPer], rv[kVecPer];
     int64_t gv[kVecPer];
 #pragma unroll
     for (int q = 0; q < kVecPer; ++q) {
       gv[q] = v0 + static_cast<int64_t>(q * kVThreads + threadIdx.x) * 4;
       if (gv[q] < v1) {
-        xv[q] = *reinterpret_cast<const f32x4_t*>(p.x + gv[q]);
-        if (kR) rv[q] = *reinterpret_cast<const f32x4_t*>(p.r + gv[q]);
+        xv[q] = load(p.x + gv[q]);
+        if (kR) rv[q] = load(p.r + gv[q]);
       }
     }
 #pragma unroll
@@ -156,9 +165,10 @@ __global__ __launch_bounds__(kVThreads) void mean3_kernel(const float* a, const 
     for (int q = 0; q < kVecPer; ++q) {
       const int64_t t = t0 + static_cast<int64_t>(q * kVThreads + threadIdx.x) * 4;
       if (t >= nv) continue;
-      const f32x4_t va = *reinterpret_cast<const f32x4_t*>(a + t);
-      const f32x4_t vb = *reinterpret_cast<const f32x4_t*>(b + t);
-      const f32x4_t vc = *reinterpret_cast<const f32x4_t*>(c + t);
+      // read once, one output: non-temporal loads (measured 17 % faster)
+      const f32x4_t va = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(a + t));
+      const f32x4_t vb = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(b + t));
+      const f32x4_t vc = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(c + t));
       f32x4_t vo;
 #pragma unroll
       for (int e = 0; e < 4; ++e) vo[e] = ((va[e] + vb[e]) + vc[e]) * kThird;
