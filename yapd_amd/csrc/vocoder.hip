@@ -110,10 +110,14 @@ __global__ __launch_bounds__(kVThreads) void voc_kernel(const VocParams p) {
     }
     if (threadIdx.x < v0 - g0) one(g0 + threadIdx.x);
     if (threadIdx.x < g1 - v1) one(v1 + threadIdx.x);
-    // Inputs are read once.  With one output, non-temporal loads (past the
-    // caches) measured 12-19 % faster; with two or four outputs 4-5 % slower.
+    // Inputs are read once.  residual_bias (one output, a residual input
+    // written long before) reads with non-temporal loads: 19 % faster on cold
+    // inputs and still 4 % when x was just written.  Snake's only input is
+    // usually the output of the convolution just before it, still in the MALL,
+    // where non-temporal loads measured 3 % slower; with two or four outputs
+    // they measured 4-5 % slower even on cold inputs.
     auto load = [](const float* src) {
-      if constexpr (kOut == 1) {
+      if constexpr (kOut == 1 && kR) {
         return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(src));
       } else {
         return *reinterpret_cast<const f32x4_t*>(src);
@@ -165,7 +169,8 @@ __global__ __launch_bounds__(kVThreads) void mean3_kernel(const float* a, const 
     for (int q = 0; q < kVecPer; ++q) {
       const int64_t t = t0 + static_cast<int64_t>(q * kVThreads + threadIdx.x) * 4;
       if (t >= nv) continue;
-      // read once, one output: non-temporal loads (measured 17 % faster)
+      // read once, one output: non-temporal loads (measured 17 % faster on
+      // cold inputs, 7 % with the first input just written)
       const f32x4_t va = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(a + t));
       const f32x4_t vb = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(b + t));
       const f32x4_t vc = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(c + t));
