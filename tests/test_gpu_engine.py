@@ -101,6 +101,25 @@ def test_ragged_starts_shuffled_pages_graph_and_head(dev, one_layer):
     assert torch.equal(hid_g2.cpu(), hid_e2.cpu())
 
 
+@pytest.mark.parametrize("lps", [[100, 177, 256], [100, 1100, 1300]])  # rows > 1024 keys are split
+def test_graph_replay_with_and_without_split_rows(dev, one_layer, lps):
+    """The engine captures its step with and without the split-KV merge launch
+    and replays the one the current plan needs; both equal the eager path."""
+    model = one_layer
+    B, bl = 3, 32
+    g = torch.Generator().manual_seed(2)
+    prefixes = [torch.randn(1, lp, 1024, generator=g).bfloat16().to(dev) for lp in lps]
+    block = torch.randn(B, bl, 1024, generator=g).bfloat16().to(dev)
+    eng = HipEngine(model, 2048, torch.bfloat16, batch_size=B)
+    sos = eng.prefix_forward(prefixes)
+    hid = eng.block_forward(block, lps).cpu()
+    eng.capture_cuda_graph(bl, speech_head=model.speech_head)
+    eng.set_shift_ctx(sos)
+    hid_g, _ = eng.block_forward_graph(block, lps)
+    assert (eng._g_plan.n_merge_live > 0) == (max(lps) + bl > 1024)
+    assert torch.equal(hid_g.cpu(), hid)
+
+
 def test_thirty_layers_block_step(dev):
     # 30 layers, 16 CFG pairs = 32 rows, prefixes U[150, 600] (pairs share a
     # length), shuffled page table, block 32, speech head V = 8194.

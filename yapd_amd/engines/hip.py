@@ -142,7 +142,7 @@ class HipEngine:
 
         # ---- graph state ----
         self._use_cuda_graph = False
-        self._graph = None
+        self._graphs: Dict[bool, torch.cuda.CUDAGraph] = {}  # keyed by "plan splits a row"
         self._g_bl = 0
         self._g_plan: Optional[_GraphPlan] = None
         self._g_cs_key = None
@@ -231,11 +231,12 @@ class HipEngine:
         if min(starts) < 0:
             raise ValueError("negative cache start")
 
-    def _workspace(self, buf: _Buffers, plan: "AttnPlan | _GraphPlan") -> kernels.T3Workspace:
+    def _workspace(self, buf: _Buffers, plan: "AttnPlan | _GraphPlan", merge: bool = True) -> kernels.T3Workspace:
+        n_merge = 0 if plan.merge is None or not merge else int(plan.merge.shape[0])
         return kernels.T3Workspace(
             buf.residual.data_ptr(), buf.q.data_ptr(), buf.attn.data_ptr(), buf.normed.data_ptr(),
             buf.delta.data_ptr(), buf.act.data_ptr(), plan.work.data_ptr(), int(plan.work.shape[0]),
-            kernels.ptr(plan.merge), 0 if plan.merge is None else int(plan.merge.shape[0]),
+            kernels.ptr(plan.merge), n_merge,
             kernels.ptr(getattr(plan, "counts", None)), kernels.ptr(plan.part_o), kernels.ptr(plan.part_ml),
             int(plan.n_slots))
 
@@ -254,8 +255,10 @@ class HipEngine:
 
     def _run(self, buf: _Buffers, plan, kv_len_dev: Tensor, *, causal: bool = False,
              head_w: Optional[Tensor] = None, shift_ctx: Optional[Tensor] = None,
-             logits: Optional[Tensor] = None, row0: int = 0, table: Optional[Tensor] = None) -> None:
-        ws = self._workspace(buf, plan)
+             logits: Optional[Tensor] = None, row0: int = 0, table: Optional[Tensor] = None,
+             merge: bool = True) -> None:
+        """``merge=False`` leaves out the split-KV merge launch (only for a plan that splits no row)."""
+        ws = self._workspace(buf, plan, merge)
         V = 0 if head_w is None else int(head_w.shape[0])
         c_model = self._descriptor(row0, table)
         kernels.check(kernels.load_library().yapd_t3_block_forward(
@@ -385,14 +388,18 @@ class HipEngine:
             self._g_shift_ctx = torch.zeros(B, 1, D, dtype=self._dtype, device=self._device)
             self._g_logits_buf = torch.zeros(B, bl, pitch, dtype=self._dtype, device=self._device)
             self._g_logits = self._g_logits_buf[..., :V]
-        body = lambda: self._run(buf, self._g_plan, self._g_plan.kv_len, head_w=self._head_w,
-                                 shift_ctx=self._g_shift_ctx, logits=self._g_logits)
-        body()  # warm-up outside the graph
+        body = lambda merge: self._run(buf, self._g_plan, self._g_plan.kv_len, head_w=self._head_w,
+                                       shift_ctx=self._g_shift_ctx, logits=self._g_logits, merge=merge)
+        body(True)  # warm-up outside the graph
         torch.cuda.synchronize(self._device)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            body()
-        self._graph = graph
+        # Two graphs: one with the split-KV merge launch, and one without for
+        # plans that split no row (the host knows which when it plans).
+        self._graphs = {}
+        for merge in (True, False):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                body(merge)
+            self._graphs[merge] = graph
         self._use_cuda_graph = True
         logger.info("HipEngine: graph captured (block=%d, batch=%d, head=%s)", bl, B, self._head_w is not None)
 
@@ -415,7 +422,7 @@ class HipEngine:
         buf = self._buffers(B, bl)
         buf.emb.copy_(block_emb.reshape(B * bl, D))
         self._update_graph_inputs(self._starts(cache_starts, B))
-        self._graph.replay()
+        self._graphs[self._g_plan.n_merge_live > 0].replay()
         return buf.hidden.view(B, bl, D), self._g_logits
 
 
@@ -446,4 +453,5 @@ class _GraphPlan:
         if merge.shape[0]:
             self.merge[: merge.shape[0]].copy_(torch.from_numpy(merge))
         self.counts.copy_(torch.tensor([work.shape[0], merge.shape[0]], dtype=torch.int32))
+        self.n_merge_live = int(merge.shape[0])  # rows split by the current plan (host copy)
         self.kv_len.copy_(torch.tensor(kv_len, dtype=torch.int32))

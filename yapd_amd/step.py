@@ -16,7 +16,7 @@ buffers overwritten by the next replay.
 
 from __future__ import annotations
 
-from typing import List, Optional
+from typing import Dict, List, Optional
 
 import torch
 
@@ -41,16 +41,16 @@ class DecodeStep:
                                   omnivoice_t_shift=omnivoice_t_shift, cfg_scale=cfg_scale, device=self.dev)
         self.xt = torch.full((n_pairs, block_size), mask_id, dtype=torch.int64, device=self.dev)
         self.k_step = torch.zeros(n_pairs, dtype=torch.int64, device=self.dev)
-        self._graph: Optional[torch.cuda.CUDAGraph] = None
+        self._graphs: Dict[bool, torch.cuda.CUDAGraph] = {}  # keyed by "plan splits a row"
         self.result: Optional[ScoreResult] = None
 
-    def _body(self) -> None:
+    def _body(self, merge: bool = True) -> None:
         eng = self.engine
         buf = eng._buffers(eng.batch_size, self.bl)
         toks = torch.cat([self.xt, self.xt], 0).view(-1)
         torch.index_select(self.emb_table, 0, toks, out=buf.emb)
         eng._run(buf, eng._g_plan, eng._g_plan.kv_len, head_w=eng._head_w, shift_ctx=eng._g_shift_ctx,
-                 logits=eng._g_logits)
+                 logits=eng._g_logits, merge=merge)
         self.result = self.scorer(eng._g_logits, self.xt, self.k_step, layout="stacked")
 
     def capture(self, cache_starts: List[int], shift_ctx: torch.Tensor) -> None:
@@ -62,14 +62,17 @@ class DecodeStep:
         self.set_cache_starts(cache_starts)
         self._body()  # warm-up outside the graph
         torch.cuda.synchronize(self.dev)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self._body()
-        self._graph = g
+        # with and without the split-KV merge launch; each replay takes the one
+        # its current attention plan needs
+        for merge in (True, False):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._body(merge)
+            self._graphs[merge] = g
 
     def set_cache_starts(self, cache_starts: List[int]) -> None:
         self.engine._update_graph_inputs(list(cache_starts))
 
     def replay(self) -> ScoreResult:
-        self._graph.replay()
+        self._graphs[self.engine._g_plan.n_merge_live > 0].replay()
         return self.result
