@@ -90,9 +90,12 @@ def test_gemm_head_shift(dev, rows):
     assert rel_err(logits.cpu(), ref) <= 8e-3
 
 
-@pytest.mark.parametrize("rows", [3, 180])  # 180 x 32 rows: large-tile path
-def test_gemm_qkv_rope_kv(dev, rows):
-    H, D, bl = 16, 1024, 32
+# 180 x 32 rows: large-tile path.  6 heads at 320 x 32 rows: 256-column tiles
+# straddle the q/k boundary (q = columns [0, 384)) and one tile holds only V
+# columns (no RoPE rows staged); 2 heads: q, k and v inside one small tile.
+@pytest.mark.parametrize("rows,H", [(3, 16), (180, 16), (320, 6), (3, 2)])
+def test_gemm_qkv_rope_kv(dev, rows, H):
+    D, bl = 1024, 32
     M = rows * bl
     A = rnd(M, D, seed=11)
     Wqkv = rnd(3 * H * 64, D, std=0.02, seed=12)

@@ -238,6 +238,9 @@ __device__ __forceinline__ void epilogue_qkv(const GemmParams& p, const f32x16_t
 #pragma unroll
   for (int q2 = 0; q2 < T::TN / 2; ++q2) {
     const int nb = n_base + 64 * q2;
+    // Columns past N (a last tile wider than what is left of 3 * HD) belong to
+    // no head: skip them (N is a multiple of 64, so a group is all in or out).
+    if (nb >= p.N) continue;
     const int section = nb / HD;  // 0 q, 1 k, 2 v
     if (section == 0) {
       epilogue_qkv_section<T, 0>(p, acc, meta, rope, m0, nb, q2, wm, lane);
