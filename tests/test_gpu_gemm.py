@@ -36,7 +36,9 @@ def test_gemm_bf16(dev, M, N, K):
     assert rel_err(out.cpu(), ref) <= 8e-3
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 1024, 1024), (16384 // 8, 1024, 4096), (4100, 1024, 1024)])
+# (16384, 1000, 1024): 256 x 256 tiles with a partial last column tile
+@pytest.mark.parametrize("M,N,K", [(200, 1024, 1024), (16384 // 8, 1024, 4096), (4100, 1024, 1024),
+                                   (16384, 1000, 1024)])
 def test_gemm_residual_equals_separate_add(dev, M, N, K):
     """The fused residual add is bit-identical to the projection stored in bf16
     followed by the bf16 residual add (HF's two roundings)."""
@@ -63,10 +65,10 @@ def test_gemm_padded_ldc_and_strided_a(dev):
     assert torch.count_nonzero(out_full[:, N:]) == 0  # nothing written past N
 
 
-@pytest.mark.parametrize("M,K", [(300, 1024), (2000, 1024),  # 2000: large-tile path, one round of tiles
-                                 (4100, 1024), (4100, 256)])  # several rounds (persistent kernel); ragged M; K < 16 k-tiles
-def test_gemm_swiglu(dev, M, K):
-    Fd = 4096
+@pytest.mark.parametrize("M,K,Fd", [(300, 1024, 4096), (2000, 1024, 4096),  # 2000: large tiles, one round
+                                     (4100, 1024, 4096), (4100, 256, 4096),  # several rounds; ragged M; K < 16 k-tiles
+                                     (8192, 1024, 1088)])  # large tiles, the last one half past 2F
+def test_gemm_swiglu(dev, M, K, Fd):
     A = rnd(M, K, seed=5)
     Wg = rnd(Fd, K, std=0.02, seed=6)
     Wu = rnd(Fd, K, std=0.02, seed=7)

@@ -12,7 +12,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M,N,K", [(256, 3072, 1024), (8192, 1024, 4096), (37, 200, 128)])
+# (16384, 1000, 1024): the large-M kernel with a partial last column tile
+@pytest.mark.parametrize("M,N,K", [(256, 3072, 1024), (8192, 1024, 4096), (37, 200, 128), (16384, 1000, 1024)])
 def test_qgemm_vs_fp32_dequant(dev, bits, M, N, K):
     g = torch.Generator().manual_seed(M + N + bits)
     w = torch.randn(N, K, generator=g) * 0.02
