@@ -60,7 +60,7 @@ def test_kv_write_strided_views(dev):
     assert torch.equal(pool.cpu(), pool_ref)
 
 
-def build_case(rows, bl, lengths, seed, n_pages=None):
+def build_case(rows, bl, lengths, seed, n_pages=None, H=H):
     """Pool filled through the oracle's scatter; returns everything the kernel needs."""
     g = torch.Generator().manual_seed(seed)
     kv_len = [L + bl for L in lengths]
@@ -83,12 +83,12 @@ def reference(q, Ks, Vs):
     out = []
     for r in range(q.shape[0]):
         o = OL._sdpa(q[r].float(), Ks[r].float(), Vs[r].float(), causal=False)
-        out.append(o.view(q.shape[1], H, 64))
+        out.append(o.view(q.shape[1], q.shape[2], 64))
     return torch.stack(out)
 
 
 def run_gpu(dev, q, pool, table, kv_len, target_items, min_split_keys=128):
-    plan = AttnPlan(kv_len, q.shape[1], H, dev, target_items=target_items, min_split_keys=min_split_keys)
+    plan = AttnPlan(kv_len, q.shape[1], q.shape[2], dev, target_items=target_items, min_split_keys=min_split_keys)
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
     plan.run(q.to(dev), pool.to(dev), torch.from_numpy(table).to(dev), out, 0.125)
     torch.cuda.synchronize()
@@ -106,6 +106,19 @@ def test_attention_matches_oracle(dev, bl, split):
         assert plan.n_slots > 0  # the split-KV merge path ran
     ref = reference(q, Ks, Vs)
     err = (out.float() - ref).abs().max().item()
+    assert err <= 2e-2, err
+
+
+@pytest.mark.parametrize("heads", [4, 8])  # one and two four-head workgroups per item
+@pytest.mark.parametrize("split", [False, True])
+def test_attention_head_counts(dev, heads, split):
+    rows, bl = 5, 16
+    lengths = log_uniform_lengths(rows, 64, 700, seed=heads)
+    q, pool, table, kv_len, Ks, Vs = build_case(rows, bl, lengths, seed=heads + int(split), H=heads)
+    out, plan = run_gpu(dev, q, pool, table, kv_len, 4096 if split else 1024, 32 if split else 128)
+    if split:
+        assert plan.n_slots > 0  # the split-KV merge path ran
+    err = (out.float() - reference(q, Ks, Vs)).abs().max().item()
     assert err <= 2e-2, err
 
 
