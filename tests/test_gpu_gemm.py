@@ -132,8 +132,9 @@ def test_gemm_qkv_rope_kv(dev, rows, H):
 
 
 @pytest.mark.parametrize("with_delta", [False, True])
-def test_rmsnorm(dev, with_delta):
-    M, D = 333, 1024
+@pytest.mark.parametrize("D", [1024, 512, 1536, 2048])  # one to four 512-wide chunks per row
+def test_rmsnorm(dev, with_delta, D):
+    M = 333
     x = rnd(M, D, seed=13) * 3
     w = (torch.rand(D, generator=torch.Generator().manual_seed(14)) + 0.5).bfloat16()
     delta = rnd(M, D, seed=15)
