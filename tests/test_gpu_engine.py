@@ -66,6 +66,28 @@ def test_one_layer_prefix_and_block(dev):
     assert hidden_ok(sos, outs["bf16"][0], outs["fp32"][0], "1-layer prefix SOS hidden")
 
 
+def test_other_model_dims(dev):
+    # hidden 512 (one 512-wide RMSNorm chunk), 8 heads (two four-head attention
+    # workgroups, QKV N = 1536), FFN 1536; two ragged rows
+    D, H, Fd = 512, 8, 1536
+    model = make_t3(n_layers=1, hidden=D, heads=H, ffn=Fd, seed=4, norm_jitter=True, device=dev)
+    B, bl, lps = 2, 16, [90, 200]
+    g = torch.Generator().manual_seed(4)
+    prefixes = [torch.randn(1, lp, D, generator=g).bfloat16() for lp in lps]
+    block = torch.randn(B, bl, D, generator=g).bfloat16()
+    eng = HipEngine(model, 512, torch.bfloat16, batch_size=B)
+    sos = eng.prefix_forward([p.to(dev) for p in prefixes])
+    hid = eng.block_forward(block.to(dev), lps)
+    bb16, bb32 = oracle_backbones(model, 512)
+    refs = {}
+    for name, bb in (("bf16", bb16), ("fp32", bb32)):
+        cache = OL.KVCache.empty(1, B, 512, H, 64, bb.dtype)
+        s_ref = OL.prefix_forward(bb, [p[0].to(bb.dtype) for p in prefixes], cache)
+        refs[name] = (s_ref, OL.block_forward(bb, block.to(bb.dtype), cache, lps))
+    assert hidden_ok(sos, refs["bf16"][0], refs["fp32"][0], "512-wide SOS hidden")
+    assert hidden_ok(hid, refs["bf16"][1], refs["fp32"][1], "512-wide block hidden")
+
+
 def test_ragged_starts_shuffled_pages_graph_and_head(dev, one_layer):
     model = one_layer
     B, bl = 3, 32
