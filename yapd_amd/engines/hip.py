@@ -339,6 +339,21 @@ class HipEngine:
                 sos[[r for _, r in last], 0] = hid[[i for i, _ in last], [lps[r] - 1 - c0 for _, r in last]]
         return sos
 
+    def causal_forward(self, emb: Tensor) -> Tensor:
+        """Final-normed hidden of every position of one causal chunk of batch row 0 at positions
+        0..n-1 (n <= 64), e.g. the unconditional prior pass of model.py:438-460.  Writes that row's
+        KV for those positions."""
+        n, D = emb.shape
+        if D != self._hidden or not 1 <= n <= PREFILL_CHUNK or n > self._max_seq_len:
+            raise ValueError(f"causal_forward needs [n, {self._hidden}] with 1 <= n <= {PREFILL_CHUNK}, "
+                             f"n <= max_seq_len; got {tuple(emb.shape)}")
+        buf = self._buffers(1, n)
+        buf.emb.copy_(emb.to(device=self._device, dtype=self._dtype))
+        buf.pos0.fill_(0)
+        plan = self._plan([n], n)
+        self._run(buf, plan, plan.kv_len, causal=True)
+        return buf.hidden.view(n, D).clone()
+
     # ------------------------------------------------------------------ #
     #  Block forward (engines/base.py:85-98)
     # ------------------------------------------------------------------ #
