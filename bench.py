@@ -48,6 +48,7 @@ import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
@@ -619,46 +620,89 @@ def kernel_sample(dev, N):
     print(json.dumps({"kernel_sample": "gemm_swiglu M=%d N=8192 K=1024 x3; copy %d bytes x3" % (N, COPY_BYTES)}))
 
 
-def cpu_baseline(model, eng, lps, bl, sc_in, n_layers, L):
-    """Oracle (torch on the host) on a bounded sample of the same step, scaled to 30 layers."""
-    import torch.nn.functional as Fn
+def host_cpu_info() -> dict:
+    """The host's CPU model, sockets, threads per core (lscpu) and the thread counts used."""
+    info = {"cpu_model": None, "sockets": None, "threads_per_core": None, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)), "torch_threads": torch.get_num_threads()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        out = ""
+    for line in out.splitlines():
+        key, _, val = line.partition(":")
+        key, val = key.strip(), val.strip()
+        if key == "Model name" and info["cpu_model"] is None:
+            info["cpu_model"] = val
+        elif key == "Socket(s)":
+            info["sockets"] = int(val) if val.isdigit() else val
+        elif key == "Thread(s) per core":
+            info["threads_per_core"] = int(val) if val.isdigit() else val
+    if info["cpu_model"] is None and os.path.exists("/proc/cpuinfo"):
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["cpu_model"] = line.split(":", 1)[1].strip()
+                    break
+    return info
+
+
+def cpu_baseline(model, eng, lps, bl, sc_in, n_layers, L, runs=3):
+    """Oracle (torch on the host) on a bounded sample of the same step, scaled to 30 layers:
+    ``n_layers`` decoder layers at the full batch, the speech head and the scoring, each the
+    median of ``runs`` timed runs after a warm-up, in bf16 (the step's dtype) and fp32."""
     from oracle import llama as OL
     from oracle import scoring as OS
     from oracle.schedule import omnivoice_unmask_schedule, quantile_fractions
 
-    threads = os.cpu_count() or 1
+    threads = len(os.sched_getaffinity(0)) or 1
     torch.set_num_threads(threads)
     B = len(lps)
     Bp = B // 2
-    bb = OL.backbone_from_model(model, max_pos=max(lps) + 2 * bl, dtype=torch.bfloat16)
-    cache = OL.KVCache(k=[], v=[])
     g = torch.Generator().manual_seed(99)
-    for _ in range(n_layers):
-        cache.k.append([torch.randn(lp + bl, 16, 64, generator=g).bfloat16() for lp in lps])
-        cache.v.append([torch.randn(lp + bl, 16, 64, generator=g).bfloat16() for lp in lps])
+    kv = [([torch.randn(lp + bl, 16, 64, generator=g).bfloat16() for lp in lps],
+           [torch.randn(lp + bl, 16, 64, generator=g).bfloat16() for lp in lps]) for _ in range(n_layers)]
     block = torch.randn(B, bl, 1024, generator=g).bfloat16()
     ctx = torch.randn(B, 1, 1024, generator=g).bfloat16()
-    OL.block_forward(bb, block[:2], OL.KVCache(k=[c[:2] for c in cache.k], v=[c[:2] for c in cache.v]),
-                     lps[:2], n_layers=1)  # warm-up
-    t = time.time()
-    hid = OL.block_forward(bb, block, cache, lps, n_layers=n_layers)
-    t_layers = time.time() - t
-    t = time.time()
-    logits = OL.speech_head_shift(hid, ctx, model.speech_head.weight.detach().cpu().bfloat16())
-    t_head = time.time() - t
-    t = time.time()
     sched = torch.tensor(omnivoice_unmask_schedule(bl, 10, 0.5))
     q = torch.tensor(quantile_fractions(3.0, 10), dtype=torch.float32)
-    OS.score_step(logits[:Bp].float(), logits[Bp:].float(), sc_in.xt.cpu(), sc_in.k_step.cpu(),
-                  sc_in.log_prior.cpu(), sched, q, K=10, cfg=0.5, tau=3.0, mask_id=8194, stop_id=6562)
-    t_score = time.time() - t
-    t_step = t_layers * L / n_layers + t_head + t_score
-    log(f"cpu baseline: {n_layers} layers {t_layers:.2f}s, head {t_head:.2f}s, score {t_score:.2f}s "
-        f"-> {t_step:.1f}s per step on {threads} threads")
-    return {"value": round(Bp * bl / t_step, 2), "unit": "speech tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle torch-CPU bf16 block forward of {n_layers} of {L} layers at the full "
-                      f"{B}-row batch (time x {L}/{n_layers}) + speech head + fp32 scoring; "
-                      f"{t_step:.1f} s per step"}
+    w_head = model.speech_head.weight.detach().cpu()
+
+    def median_time(fn):
+        fn()  # warm-up
+        ts = []
+        for _ in range(runs):
+            t = time.time()
+            fn()
+            ts.append(time.time() - t)
+        return sorted(ts)[len(ts) // 2]
+
+    per = {}
+    for name, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        bb = OL.backbone_from_model(model, max_pos=max(lps) + 2 * bl, dtype=dt)
+        cache = OL.KVCache(k=[[t.to(dt) for t in k] for k, _ in kv], v=[[t.to(dt) for t in v] for _, v in kv])
+        blk, cx, wh = block.to(dt), ctx.to(dt), w_head.to(dt)
+        hid = OL.block_forward(bb, blk, cache, lps, n_layers=n_layers)
+        t_layers = median_time(lambda: OL.block_forward(bb, blk, cache, lps, n_layers=n_layers))
+        logits = OL.speech_head_shift(hid, cx, wh)
+        t_head = median_time(lambda: OL.speech_head_shift(hid, cx, wh))
+        lf = logits.float()
+        t_score = median_time(lambda: OS.score_step(
+            lf[:Bp], lf[Bp:], sc_in.xt.cpu(), sc_in.k_step.cpu(), sc_in.log_prior.cpu(), sched, q, K=10, cfg=0.5,
+            tau=3.0, mask_id=8194, stop_id=6562))
+        t_step = t_layers * L / n_layers + t_head + t_score
+        per[name] = dict(t_layers=t_layers, t_head=t_head, t_score=t_score, t_step=t_step)
+        log(f"cpu baseline {name}: {n_layers} layers {t_layers:.2f}s, head {t_head:.2f}s, score {t_score:.2f}s "
+            f"(medians of {runs}) -> {t_step:.1f}s per step on {threads} threads")
+    info = host_cpu_info()
+    bf, fp = per["bf16"], per["fp32"]
+    return {"value": round(Bp * bl / bf["t_step"], 2), "unit": "speech tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle torch-CPU block forward of {n_layers} of {L} layers at the full {B}-row batch "
+                      f"(time x {L}/{n_layers}) + speech head + fp32 scoring, bf16; median of {runs} runs each "
+                      f"after a warm-up; {bf['t_step']:.1f} s per step",
+            "value_fp32": round(Bp * bl / fp["t_step"], 2),
+            "layers_timed": n_layers, "layers_total": L, "rows": B, "layer_scale": L / n_layers, "runs": runs,
+            "stat": "median", "seconds_per_step": {k: round(v["t_step"], 3) for k, v in per.items()},
+            "seconds_layers_sample": {k: round(v["t_layers"], 3) for k, v in per.items()}, **info}
 
 
 if __name__ == "__main__":

@@ -165,23 +165,46 @@ def block_forward(bb: Backbone, block_emb: torch.Tensor, cache: KVCache,
     Writes the block's K/V tentatively at ``[cs, cs+bl)`` of every row.
     ``n_layers`` limits the stack (used only for bounded CPU timing samples).
     """
-    B, bl, D = block_emb.shape
-    layers = bb.layers if n_layers is None else bb.layers[:n_layers]
+    n = len(bb.layers) if n_layers is None else n_layers
     h = block_emb.to(bb.dtype)
+    for li in range(n):
+        h = layer_forward(bb, li, h, cache, cache_starts)
+    return rms_norm(h, bb.norm, bb.norm_eps)
+
+
+def layer_forward(bb: Backbone, li: int, h: torch.Tensor, cache: KVCache,
+                  cache_starts: Sequence[int]) -> torch.Tensor:
+    """Decoder layer ``li`` of the block forward (torch_sdpa.py:274-341 per layer,
+    server/engine.py:133-176): the residual stream ``h [B, bl, D]`` entering the layer
+    -> the residual leaving it.  Writes the block's K/V of layer ``li`` at ``[cs, cs+bl)``."""
+    B, bl, D = h.shape
+    h = h.to(bb.dtype)
+    q, k, v = layer_qkv(bb, li, h, cache_starts)
+    outs = []
+    for r, cs in enumerate(cache_starts):
+        kc, vc = cache.k[li][r], cache.v[li][r]
+        kc[cs: cs + bl] = k[r]
+        vc[cs: cs + bl] = v[r]
+        outs.append(_sdpa(q[r], kc[: cs + bl], vc[: cs + bl], causal=False))
+    return layer_tail(bb, li, h, torch.stack(outs))
+
+
+def layer_qkv(bb: Backbone, li: int, h: torch.Tensor, cache_starts: Sequence[int]):
+    """First half of decoder layer ``li`` (flashinfer.py:992-1032): input RMSNorm, the fused
+    QKV projection and NeoX RoPE at positions ``cs .. cs+bl-1`` -> q, k, v ``[B, bl, H, hd]``."""
+    lw = bb.layers[li]
+    bl = h.shape[1]
     pos = torch.stack([torch.arange(cs, cs + bl) for cs in cache_starts])  # [B, bl]
     cos, sin = bb.cos[pos], bb.sin[pos]                                      # [B, bl, hd]
-    for li, lw in enumerate(layers):
-        hn = rms_norm(h, lw.ln_in, lw.eps_in)
-        q, k, v = _split_qkv(bb, F.linear(hn, lw.wqkv))
-        q, k = rope(q, cos, sin), rope(k, cos, sin)
-        outs = []
-        for r, cs in enumerate(cache_starts):
-            kc, vc = cache.k[li][r], cache.v[li][r]
-            kc[cs: cs + bl] = k[r]
-            vc[cs: cs + bl] = v[r]
-            outs.append(_sdpa(q[r], kc[: cs + bl], vc[: cs + bl], causal=False))
-        h = _layer_tail(bb, lw, h, torch.stack(outs))
-    return rms_norm(h, bb.norm, bb.norm_eps)
+    hn = rms_norm(h.to(bb.dtype), lw.ln_in, lw.eps_in)
+    q, k, v = _split_qkv(bb, F.linear(hn, lw.wqkv))
+    return rope(q, cos, sin), rope(k, cos, sin), v
+
+
+def layer_tail(bb: Backbone, li: int, h: torch.Tensor, attn: torch.Tensor) -> torch.Tensor:
+    """Second half of decoder layer ``li`` (flashinfer.py:1040-1060): o_proj and the residual
+    add, post-attention RMSNorm, SwiGLU MLP and its residual add -> the residual leaving it."""
+    return _layer_tail(bb, bb.layers[li], h.to(bb.dtype), attn.to(bb.dtype))
 
 
 def prefix_forward(bb: Backbone, embs: Sequence[torch.Tensor], cache: KVCache) -> torch.Tensor:

@@ -18,15 +18,21 @@ consecutive tokens of one V column with a single vector load.
 
 from __future__ import annotations
 
-from typing import List, Sequence, Tuple
+from typing import List, Sequence, Tuple, Union
 
 import numpy as np
 import torch
 
 
-def page_write_indices(table: Sequence[Sequence[int]], cache_starts: Sequence[int], bl: int,
+def page_write_indices(table: Sequence[Sequence[int]], cache_starts: Union[int, Sequence[int]], bl: int,
                        ps: int = 16) -> Tuple[np.ndarray, np.ndarray]:
-    """Flat (page, slot) for the ``B*bl`` block tokens (engines/flashinfer.py:318-344)."""
+    """Flat (page, slot) for the ``B*bl`` block tokens (engines/flashinfer.py:318-344).
+
+    ``cache_starts`` is one start for every row or a per-row list, as in the
+    reference; with the identity table ``table[r][j] = r*P + j`` this is the
+    reference's ``r*P + pos//ps``, ``pos % ps``."""
+    if isinstance(cache_starts, (int, np.integer)):
+        cache_starts = [int(cache_starts)] * len(table)
     pages: List[int] = []
     slots: List[int] = []
     for r, cs in enumerate(cache_starts):
@@ -37,8 +43,11 @@ def page_write_indices(table: Sequence[Sequence[int]], cache_starts: Sequence[in
     return np.asarray(pages, dtype=np.int64), np.asarray(slots, dtype=np.int64)
 
 
-def plan(table: Sequence[Sequence[int]], kv_lens: Sequence[int], bl: int, ps: int = 16):
-    """``qo_indptr``, ``kv_indptr``, ``kv_indices``, ``last_page_len`` (engines/flashinfer.py:346-411)."""
+def plan(table: Sequence[Sequence[int]], kv_lens: Union[int, Sequence[int]], bl: int, ps: int = 16):
+    """``qo_indptr``, ``kv_indptr``, ``kv_indices``, ``last_page_len`` (engines/flashinfer.py:346-411):
+    each row's ``ceil(kv_len/ps)`` pages in table order, ``last_page_len = kv_len % ps or ps``."""
+    if isinstance(kv_lens, (int, np.integer)):
+        kv_lens = [int(kv_lens)] * len(table)
     B = len(kv_lens)
     qo = np.zeros(B + 1, dtype=np.int32)
     kvi = np.zeros(B + 1, dtype=np.int32)

@@ -169,3 +169,57 @@ def test_ragged_stress_shape(dev):
         K, V = kernels.kv_gather(pool, tab[r], kv_len[r])
         ref = OL._sdpa(q[r].float().cpu(), K.float().cpu(), V.float().cpu(), causal=False).view(bl, H, 64)
         assert (out[r].float().cpu() - ref).abs().max().item() <= 2e-2
+
+
+def reference_causal(q, Ks, Vs, kv_len, bl):
+    """Query i of a row's block sees keys < kv_len - bl + i + 1 (prefix prefill)."""
+    out = []
+    for r in range(q.shape[0]):
+        kvl = kv_len[r]
+        mask = torch.arange(kvl)[None, :] <= (kvl - bl + torch.arange(bl))[:, None]
+        s = torch.einsum("qhd,khd->hqk", q[r].float(), Ks[r].float()) * 0.125
+        s = s.masked_fill(~mask[None], float("-inf"))
+        o = torch.einsum("hqk,khd->qhd", s.softmax(-1), Vs[r].float())
+        out.append(o)
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("bl", [16, 64])
+def test_causal_split_items_shorter_than_the_block(dev, bl):
+    """Causal attention split into 32-key items with kv_len % 32 != 0: the last
+    item is shorter than the block, so the first queries see none of its keys
+    (their partial has m = -inf, l = 0); the merge must skip it, not turn it
+    into NaN."""
+    rows = 3
+    lengths = [5 + 64, 5 + 160, 21 + 320]  # kv_len % 32 = 5, 5, 21 (plus bl, a multiple of 16)
+    q, pool, table, kv_len, Ks, Vs = build_case(rows, bl, lengths, seed=40 + bl)
+    assert all(k % 32 not in (0,) for k in kv_len)
+    plan = AttnPlan(kv_len, bl, H, dev, target_items=4096, min_split_keys=32)
+    assert plan.n_slots > 0
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
+    plan.run(q.to(dev), pool.to(dev), torch.from_numpy(table).to(dev), out, 0.125, causal=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    err = (out.cpu().float() - reference_causal(q, Ks, Vs, kv_len, bl)).abs().max().item()
+    assert err <= 2e-2, err
+
+
+def test_plan_longer_than_device_kv_len(dev):
+    """The serving engine plans from upper bounds of the cache length and the
+    kernel masks by the true device length: items wholly past it see no key."""
+    rows, bl = 3, 16
+    lengths = [40, 300, 1100]
+    q, pool, table, kv_len, Ks, Vs = build_case(rows, bl, lengths, seed=44)
+    slack = [200, 64, 40]  # the first row's last items lie entirely past its true length
+    plan = AttnPlan([k + s for k, s in zip(kv_len, slack)], bl, H, dev, target_items=4096, min_split_keys=32)
+    assert plan.n_slots > 0
+    kv_dev = torch.tensor(kv_len, dtype=torch.int32, device=dev)
+    ppr = max((k + s + 15) // 16 for k, s in zip(kv_len, slack))
+    tab = torch.zeros(rows, ppr, dtype=torch.int32)
+    tab[:, : table.shape[1]] = torch.from_numpy(table)
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
+    kernels.attn_paged_block(q.to(dev), pool.to(dev), tab.to(dev), kv_dev, plan.work, plan.merge, plan.part_o,
+                             plan.part_ml, out, 0.125)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert (out.cpu().float() - reference(q, Ks, Vs)).abs().max().item() <= 2e-2

@@ -216,6 +216,16 @@ def test_fused_snake_module_paths(dev):
     assert install_fused_snake(holder) == 2
     torch.testing.assert_close(holder.a(x), want_a, rtol=1e-5, atol=1e-5)  # log-scale alpha through the kernel
     torch.testing.assert_close(holder.b(x), want_b, rtol=1e-5, atol=1e-5)
-    # a non-contiguous input takes the module's torch expression, as in the reference
+    # a strided input is copied to a contiguous one and runs the same kernel
+    # (there is no torch-expression path)
     xt = x.transpose(1, 2).contiguous().transpose(1, 2)
+    assert not xt.is_contiguous()
+    assert torch.equal(holder.b(xt), holder.b(xt.contiguous()))
     torch.testing.assert_close(holder.b(xt), want_t, rtol=1e-5, atol=1e-5)
+    # inputs the kernels cannot take raise instead of falling back to torch
+    with pytest.raises(RuntimeError, match="contiguous fp32 CUDA BCT required"):
+        holder.b(x.double())
+    with pytest.raises(RuntimeError, match="contiguous fp32 CUDA BCT required"):
+        holder.b(x.cpu())
+    with pytest.raises(RuntimeError, match="contiguous fp32 CUDA BCT required"):
+        holder.b(x[0])

@@ -25,6 +25,7 @@
 #include <numeric>
 #include <vector>
 
+#include "attention.h"
 #include "common.h"
 #include "kv_layout.h"
 
@@ -46,6 +47,7 @@ struct AttnParams {
   const int32_t* counts;  // optional device {n_work, n_merge}: grids sized by upper bounds (graph replay)
   float* part_o;        // [slots, bl, H, 64]
   float* part_ml;       // [slots, bl, H, 2]
+  int n_slots;          // partials exist for slots [0, n_slots); an item naming another slot writes nothing
   float scale_log2;     // softmax scale * log2(e)
   int causal;           // 1: query i of the block sees keys < kv_len - bl + i + 1 (prefix prefill)
   uint16_t* out;        // [rows, bl, H, 64]
@@ -215,12 +217,17 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
       for (int i = 1; i < 8; ++i) cm = fmaxf(cm, sv[i]);
       cm = max_xor16_32(cm);
       const float mn = fmaxf(m[qt], cm);
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+      // A query that has seen no key yet (every score so far -inf: a split
+      // item past the query's causal limit, or a plan longer than the device
+      // kv_len) keeps m = -inf; exponents taken against 0 then give alpha = 0
+      // and p = 0 instead of exp2(-inf - -inf) = NaN, so its l and O stay 0.
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] - mref);
       float ps = 0.f;
       float p[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(sv[i] - mn);
+        p[i] = __builtin_amdgcn_exp2f(sv[i] - mref);
         ps += p[i];
       }
       l[qt] = l[qt] * alpha + ps;
@@ -252,7 +259,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
     if (q >= bl) continue;
     const int64_t row_q = (static_cast<int64_t>(r) * bl + q) * H + h;
     if (slot < 0) {
-      const float inv = 1.f / L;
+      // L = 0 only for a query that sees no key at all (an empty row): zeros, not NaN
+      const float inv = L > 0.f ? 1.f / L : 0.f;
       uint16_t* op = P.out + row_q * kHeadDim + 4 * g;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
@@ -261,7 +269,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParam
         w2[1] = pack_bf16x2(o[qt][mt][2] * inv, o[qt][mt][3] * inv);
         *reinterpret_cast<u32x2_t*>(op + 16 * mt) = w2;
       }
-    } else {
+    } else if (slot < P.n_slots) {
       const int64_t prow = (static_cast<int64_t>(slot) * bl + q) * H + h;
       float* pp = P.part_o + prow * kHeadDim + 4 * g;
 #pragma unroll
@@ -280,10 +288,13 @@ struct MergeParams {
   const float* part_o;
   const float* part_ml;
   int bl, H;
+  int n_slots;  // parts outside [0, n_slots) are skipped
   uint16_t* out;
 };
 
 __device__ __forceinline__ void merge_one(const MergeParams& P, int3 mi, int q) {
+  mi.y = max(mi.y, 0);
+  mi.z = max(min(mi.z, P.n_slots - mi.y), 0);  // a merge record past the partials reads nothing
   for (int t = threadIdx.x; t < P.H * 16; t += blockDim.x) {
     const int h = t >> 4;
     const int d0 = (t & 15) * 4;
@@ -296,11 +307,13 @@ __device__ __forceinline__ void merge_one(const MergeParams& P, int3 mi, int q) 
     float L = 0.f;
     for (int s = 0; s < mi.z; ++s) {
       const int64_t prow = (static_cast<int64_t>(mi.y + s) * P.bl + q) * P.H + h;
+      const float ls = P.part_ml[prow * 2 + 1];
+      if (!(ls > 0.f)) continue;  // a part in which this query saw no key
       const float w = __builtin_amdgcn_exp2f(P.part_ml[prow * 2] - M);
-      L += w * P.part_ml[prow * 2 + 1];
+      L += w * ls;
       acc += w * *reinterpret_cast<const f32x4_t*>(P.part_o + prow * kHeadDim + d0);
     }
-    const float inv = 1.f / L;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
     u32x2_t w2;
     w2[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
     w2[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
@@ -444,11 +457,11 @@ extern "C" int yapd_attn_plan(const int32_t* kv_len, int rows, int target_items,
   return YAPD_OK;
 }
 
-extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
-                                     int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads,
-                                     const int32_t* work, int n_work, const int32_t* merge, int n_merge,
-                                     const int32_t* counts, float* part_o, float* part_ml, int n_slots,
-                                     float scale, int causal, void* out, void* stream) {
+namespace yapd {
+
+int attn_checks(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride,
+                int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads, const int32_t* work, int n_work,
+                void* out) {
   YAPD_REQUIRE(q && kv_pool && page_table && kv_len && work && out, "attn: NULL pointer");
   YAPD_REQUIRE(yapd::aligned16(q) && yapd::aligned16(kv_pool) && yapd::aligned16(out) && yapd::aligned16(work),
                "attn: q, kv_pool, out and work must be 16-byte aligned");
@@ -457,8 +470,13 @@ extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t
                yapd::kWaves);
   YAPD_REQUIRE(n_pages >= 1 && table_cols >= 1 && table_stride >= table_cols, "attn: empty pool or table");
   YAPD_REQUIRE(n_work >= 1 && n_work < (1 << 30), "attn: n_work = %d", n_work);
-  YAPD_REQUIRE(n_merge == 0 || (merge && part_o && part_ml && n_slots >= 1), "attn: split items need a workspace");
-  YAPD_REQUIRE(n_merge == 0 || (yapd::aligned16(part_o)), "attn: part_o must be 16-byte aligned");
+  return YAPD_OK;
+}
+
+int attn_launch(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride,
+                int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads, const int32_t* work, int n_work,
+                const int32_t* merge, int n_merge, const int32_t* counts, float* part_o, float* part_ml, int n_slots,
+                float scale, int causal, void* out, void* stream) {
   yapd::AttnParams P;
   P.q = static_cast<const uint16_t*>(q);
   P.pool = static_cast<const uint16_t*>(kv_pool);
@@ -474,6 +492,7 @@ extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t
   P.counts = counts;
   P.part_o = part_o;
   P.part_ml = part_ml;
+  P.n_slots = (part_o != nullptr && part_ml != nullptr) ? n_slots : 0;
   P.scale_log2 = scale * 1.4426950408889634f;
   P.causal = causal != 0;
   P.out = static_cast<uint16_t*>(out);
@@ -487,13 +506,29 @@ extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t
   }
   YAPD_LAUNCH_CHECK("attn_paged_kernel launch");
   if (n_merge > 0) {
-    yapd::MergeParams M{merge, counts, part_o, part_ml, bl, n_heads, static_cast<uint16_t*>(out)};
+    yapd::MergeParams M{merge, counts, part_o, part_ml, bl, n_heads, P.n_slots, static_cast<uint16_t*>(out)};
     const int64_t pairs = static_cast<int64_t>(n_merge) * bl;
     const dim3 mgrid(static_cast<unsigned>(pairs < yapd::kMergeGrid ? pairs : yapd::kMergeGrid));
     hipLaunchKernelGGL(yapd::attn_merge_kernel, mgrid, dim3(256), 0, st, M, n_merge);
     YAPD_LAUNCH_CHECK("attn_merge_kernel launch");
   }
   return YAPD_OK;
+}
+
+}  // namespace yapd
+
+extern "C" int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                                     int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads,
+                                     const int32_t* work, int n_work, const int32_t* merge, int n_merge,
+                                     const int32_t* counts, float* part_o, float* part_ml, int n_slots,
+                                     float scale, int causal, void* out, void* stream) {
+  const int rc = yapd::attn_checks(q, kv_pool, n_pages, page_table, table_stride, table_cols, kv_len, rows, bl, n_heads,
+                             work, n_work, out);
+  if (rc != YAPD_OK) return rc;
+  YAPD_REQUIRE(n_merge == 0 || (merge && part_o && part_ml && n_slots >= 1), "attn: split items need a workspace");
+  YAPD_REQUIRE(n_merge == 0 || (yapd::aligned16(part_o)), "attn: part_o must be 16-byte aligned");
+  return yapd::attn_launch(q, kv_pool, n_pages, page_table, table_stride, table_cols, kv_len, rows, bl, n_heads, work,
+                           n_work, merge, n_merge, counts, part_o, part_ml, n_slots, scale, causal, out, stream);
 }
 
 extern "C" int yapd_kv_write(const void* k, const void* v, int64_t k_tok_stride, int64_t v_tok_stride, void* kv_pool,

@@ -374,6 +374,39 @@ class HipEngine:
         self._run(buf, plan, plan.kv_len)
         return buf.hidden.view(B, bl, D).clone()
 
+    def layer_forward(self, li: int, x: Tensor, cache_starts: CacheStarts) -> Dict[str, Tensor]:
+        """Run decoder layer ``li`` alone on the residual stream ``x [B, bl, D]`` entering it
+        (teacher forcing: any input, e.g. what this engine's layer ``li-1`` produced): the same
+        native block forward with a one-layer model descriptor.  Returns the layer's rotated
+        queries ``q [B, bl, H, 64]``, its attention output ``attn [B, bl, H*64]``, the
+        ``residual`` leaving it and that residual normed by the next layer's input norm
+        (``hidden``; the final norm after the last layer).  Writes layer ``li``'s block KV at
+        ``[cs, cs+bl)``."""
+        B, bl, D = x.shape
+        if not 0 <= li < self._num_layers:
+            raise ValueError(f"layer {li} outside [0, {self._num_layers})")
+        if B != self._batch_size or D != self._hidden or not 1 <= bl <= 64:
+            raise ValueError(f"x must be ({self._batch_size}, 1..64, {self._hidden}); got {tuple(x.shape)}")
+        starts = self._starts(cache_starts, B)
+        self._check_capacity(starts, bl)
+        m = kernels.T3Model.from_buffer_copy(self._c_model)
+        m.n_layers = 1
+        m.layers = ctypes.pointer(self._c_layers[li])
+        if li + 1 < self._num_layers:
+            m.final_norm = self._w[li + 1]["ln_in"].data_ptr()
+            m.final_eps = self._w[li + 1]["eps_in"]
+        buf = self._buffers(B, bl)
+        buf.emb.copy_(x.reshape(B * bl, D))
+        buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+        plan = self._plan([s + bl for s in starts], bl)
+        ws = self._workspace(buf, plan)
+        kernels.check(kernels.load_library().yapd_t3_block_forward(
+            ctypes.byref(m), ctypes.byref(ws), buf.emb.data_ptr(), B, bl, buf.pos0.data_ptr(),
+            plan.kv_len.data_ptr(), 0, buf.hidden.data_ptr(), None, 0, None, None, 0,
+            kernels.stream_ptr(self._device)))
+        return dict(q=buf.q.view(B, bl, self._num_heads, 64).clone(), attn=buf.attn.view(B, bl, -1).clone(),
+                    residual=buf.residual.view(B, bl, D).clone(), hidden=buf.hidden.view(B, bl, D).clone())
+
     # ------------------------------------------------------------------ #
     #  Graph path (engines/base.py:100-113, 119-141)
     # ------------------------------------------------------------------ #
@@ -393,6 +426,9 @@ class HipEngine:
         self._g_bl = bl
         self._g_plan = _GraphPlan(B, bl, self._num_heads, self._device, self._attn_target)
         starts = [min(c, self._max_seq_len - bl) for c in self._cache_lens]
+        # the new plan and buffers hold nothing yet: refresh them even if the
+        # starts equal those of an earlier capture at another block size
+        self._g_cs_key = None
         self._update_graph_inputs(starts)
         if speech_head is not None:
             self._head_w = speech_head.weight.detach().to(self._dtype).contiguous()

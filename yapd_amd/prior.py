@@ -25,7 +25,8 @@ def uncond_block_prior(model, block_size: int, sos_id: int, mask_id: int, *,
                        embed: Optional[Callable[[torch.Tensor], torch.Tensor]] = None) -> torch.Tensor:
     """The ``(V,)`` fp32 prior of model.py:408-475.  ``embed`` maps a ``[1, n]`` token tensor to
     ``[1, n, D]`` input embeddings, as ``_embed_speech_tokens`` (model.py:397-402, called so at
-    :448-449); default: rows of ``model.speech_emb``."""
+    :448-449); default: the model's own ``_embed_speech_tokens`` (which adds the learned
+    position embedding when the model has one), else rows of ``model.speech_emb``."""
     bs = int(block_size)
     if not 1 <= bs <= 63:
         raise ValueError(f"block_size must be in [1, 63] (one causal chunk of 1 + block_size); got {bs}")
@@ -34,7 +35,10 @@ def uncond_block_prior(model, block_size: int, sos_id: int, mask_id: int, *,
         raise ValueError("the speech head must be bias-free (T3's is)")
     dev = head_w.device
     toks = torch.tensor([int(sos_id)] + [int(mask_id)] * bs, dtype=torch.long, device=dev)
-    emb = embed(toks.unsqueeze(0))[0] if embed is not None else model.speech_emb.weight.detach()[toks]
+    if embed is None:
+        embed = getattr(model, "_embed_speech_tokens", None) or (lambda t: model.speech_emb(t))
+    with torch.no_grad():
+        emb = embed(toks.unsqueeze(0))[0]
     eng = HipEngine(model, 64, torch.bfloat16, batch_size=1)
     hidden = eng.causal_forward(emb.to(torch.bfloat16))
     logits = torch.empty(bs, head_w.shape[0], dtype=torch.bfloat16, device=dev)

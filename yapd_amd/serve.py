@@ -34,6 +34,7 @@ from typing import Deque, List, Optional
 import torch
 
 from . import kernels
+from .embed import SpeechEmbedder
 from .engines.hip import HipEngine
 from .paged import PAGE_SIZE
 from .scoring import BlockScorer
@@ -146,7 +147,7 @@ class HipFlashEngine:
             raise ValueError("the speech head must be bias-free (T3's is)")
         self.head_w = head.weight.detach().to(torch.bfloat16).contiguous()
         self.V = int(self.head_w.shape[0])
-        self.emb_table = model.speech_emb.weight.detach().to(torch.bfloat16).contiguous()
+        self.embed = SpeechEmbedder(model, self.BS, self.dev)
         dev = self.dev
 
         # ---- per-slot state (server/engine.py:338-345) ----
@@ -256,7 +257,7 @@ class HipFlashEngine:
         torch.gather(self.xt[:A], 1, self.blk_start[:A, None] + self.ar, out=xt_blk)
         self.toks[: R * BS].view(A, nb, BS).copy_(xt_blk[:, None, :])
         buf = self.eng._buffers(R, BS)
-        torch.index_select(self.emb_table, 0, self.toks[: R * BS], out=buf.emb)
+        self.embed(self.toks[: R * BS], buf.emb)
         buf.pos0.view(A, nb).copy_(self.cache_len[:A, None])
         torch.add(buf.pos0, BS, out=self.kv_dev[:R])
         self.eng._run(buf, self.plan, self.kv_dev[:R], head_w=self.head_w, shift_ctx=self.shift_ctx[:R],

@@ -5,7 +5,7 @@ chatterbox_flash/model.py:823-900) for CFG pairs in generate()'s stacked
 row order ``[cond x Bp | null x Bp]`` (model.py:761-767, 859-860):
 
   1. embed the block tokens of every pair into both of its rows
-     (server/engine.py:497-500);
+     (``_embed_speech_tokens``, model.py:397-402, server/engine.py:497-500);
   2. 30-layer backbone + final norm + token-shifted speech head
      (HipEngine, engines/flashinfer.py:1312-1461);
   3. CFG combine + PMI + quantile unmask (kernel (c), server/engine.py:532-593).
@@ -20,6 +20,7 @@ from typing import Dict, List, Optional
 
 import torch
 
+from .embed import SpeechEmbedder
 from .engines.hip import HipEngine
 from .scoring import BlockScorer, ScoreResult
 
@@ -34,7 +35,7 @@ class DecodeStep:
         self.n_pairs = n_pairs
         self.bl = block_size
         self.dev = engine._device
-        self.emb_table = model.speech_emb.weight.detach().to(torch.bfloat16).contiguous()
+        self.embed = SpeechEmbedder(model, block_size, self.dev)
         self.speech_head = model.speech_head
         self.scorer = BlockScorer(n_pairs=n_pairs, block_size=block_size, log_prior=log_prior, mask_id=mask_id,
                                   stop_id=stop_id, num_steps=num_steps, time_shift_tau=time_shift_tau,
@@ -48,7 +49,7 @@ class DecodeStep:
         eng = self.engine
         buf = eng._buffers(eng.batch_size, self.bl)
         toks = torch.cat([self.xt, self.xt], 0).view(-1)
-        torch.index_select(self.emb_table, 0, toks, out=buf.emb)
+        self.embed(toks, buf.emb)
         eng._run(buf, eng._g_plan, eng._g_plan.kv_len, head_w=eng._head_w, shift_ctx=eng._g_shift_ctx,
                  logits=eng._g_logits, merge=merge)
         self.result = self.scorer(eng._g_logits, self.xt, self.k_step, layout="stacked")

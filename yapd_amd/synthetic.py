@@ -9,6 +9,7 @@ weights are not available offline.
 from __future__ import annotations
 
 import math
+import types
 from dataclasses import dataclass
 from typing import List, Optional
 
@@ -108,32 +109,57 @@ class SyntheticT3(torch.nn.Module):
     (bias-free Linear D -> V) and ``speech_emb`` (V + 1 rows: the extra row is
     MASK, chatterbox_flash/model.py:340-352)."""
 
-    def __init__(self, tfmr, speech_head, speech_emb):
+    def __init__(self, tfmr, speech_head, speech_emb, speech_pos_emb=None):
         super().__init__()
         self.tfmr = tfmr
         self.speech_head = speech_head
         self.speech_emb = speech_emb
+        self.hp = types.SimpleNamespace(input_pos_emb="learned" if speech_pos_emb is not None else None)
+        if speech_pos_emb is not None:
+            self.speech_pos_emb = speech_pos_emb
 
     @property
     def device(self) -> torch.device:
         return self.tfmr.norm.weight.device
 
-    def embed_speech_tokens(self, tokens: torch.Tensor) -> torch.Tensor:
-        """Speech-token embedding lookup (chatterbox_flash/model.py:397-402 without
-        the learned position embedding, which this synthetic model omits)."""
-        return self.speech_emb(tokens)
+    def _embed_speech_tokens(self, tokens: torch.Tensor) -> torch.Tensor:
+        """chatterbox_flash/model.py:397-402: the token rows, plus the learned
+        position embedding when ``hp.input_pos_emb == "learned"``."""
+        emb = self.speech_emb(tokens)
+        if self.hp.input_pos_emb == "learned":
+            emb = emb + self.speech_pos_emb(tokens)
+        return emb
+
+    embed_speech_tokens = _embed_speech_tokens
+
+
+class LearnedPositions(torch.nn.Module):
+    """Learned position table with chatterbox-tts's call convention (the
+    ``speech_pos_emb`` that model.py:401 adds): ``forward(tokens [B, n])`` returns
+    the rows of positions ``0 .. n-1`` -- positions inside the tensor passed,
+    whatever the tokens are.  chatterbox-tts 0.1.7 is not installed here, so
+    this convention is restated from its published module, not checked
+    against it."""
+
+    def __init__(self, n_positions: int, dim: int, device=None, dtype=None):
+        super().__init__()
+        self.emb = torch.nn.Embedding(n_positions, dim, device=device, dtype=dtype)
+
+    def forward(self, tokens: torch.Tensor) -> torch.Tensor:
+        return self.emb(torch.arange(tokens.shape[1], device=tokens.device))
 
 
 def make_t3(*, n_layers: int = 30, hidden: int = 1024, heads: int = 16, ffn: int = 4096,
             vocab: int = SPEECH_VOCAB, rope_theta: float = 10000.0, rope_parameters: Optional[dict] = None,
             eps: float = 1e-5, max_positions: int = 8192, seed: int = 0, dtype=torch.bfloat16, device="cpu",
-            norm_jitter: bool = False, weight_std: float = 0.02) -> SyntheticT3:
+            norm_jitter: bool = False, weight_std: float = 0.02, learned_pos_emb: bool = False) -> SyntheticT3:
     """Random-init T3 backbone with a fixed draw order.
 
     Per layer, in order: q, k, v, o, gate, up, down ~ N(0, weight_std); then
     (if ``norm_jitter``) input/post-attention RMSNorm gains ~ U(0.5, 1.5),
     else 1 (HF init).  Then the final-norm gain (same rule), speech head
-    ~ N(0, weight_std) and speech embeddings ~ N(0, 1).
+    ~ N(0, weight_std) and speech embeddings ~ N(0, 1); with ``learned_pos_emb``
+    last a learned speech position table (``max_positions`` rows) ~ N(0, 0.02).
     """
     from transformers import LlamaConfig, LlamaModel
     from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
@@ -177,4 +203,8 @@ def make_t3(*, n_layers: int = 30, hidden: int = 1024, heads: int = 16, ffn: int
         head.weight.copy_(normal((vocab, hidden), weight_std))
         emb = torch.nn.Embedding(vocab + 1, hidden, device=device, dtype=dtype)
         emb.weight.copy_(normal((vocab + 1, hidden), 1.0))
-    return SyntheticT3(tf, head, emb).eval()
+        pos = None
+        if learned_pos_emb:
+            pos = LearnedPositions(max_positions, hidden, device=device, dtype=dtype)
+            pos.emb.weight.copy_(normal((max_positions, hidden), 0.02))
+    return SyntheticT3(tf, head, emb, pos).eval()

@@ -22,8 +22,11 @@ Two deliberate differences: an ``alpha_logscale`` Snake runs the kernel on
 ``exp(alpha)`` (the reference falls back to torch ops there, and in the fused
 resblock passes the log-scale alpha of the next activation unconverted,
 server/kernels.py:118), and all tensors of one call must be on one device.
-Inputs that are not contiguous 3-D fp32 GPU tensors take the module's own
-torch expression, as in the reference (server/kernels.py:110-112, 120).
+The installed forwards have no torch-expression path (the reference falls
+back to one for inputs its kernels do not take, server/kernels.py:110-112,
+120, 142-146): a strided fp32 [B, C, T] GPU tensor is copied to a contiguous
+one, any other input raises, and a generator whose decode averages other than
+three resblocks is refused at install time.
 """
 
 from __future__ import annotations
@@ -36,9 +39,6 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels
-
-NO_DIV_BY_ZERO = 1e-9
-
 
 def _bct_ok(x: torch.Tensor) -> bool:
     """What the kernels take: a contiguous 3-D fp32 GPU tensor."""
@@ -165,20 +165,17 @@ def _alpha(snake: torch.nn.Module) -> torch.Tensor:
     return a.float().contiguous()
 
 
-def _snake_expr(snake: torch.nn.Module, x: torch.Tensor) -> torch.Tensor:
-    """The module's own torch expression, for inputs the kernel does not take."""
-    a = snake.alpha.unsqueeze(0).unsqueeze(-1)
-    if getattr(snake, "alpha_logscale", False):
-        a = torch.exp(a)
-    bias = getattr(snake, "pre_bias", None)
-    if bias is not None:
-        x = x + bias.unsqueeze(0).unsqueeze(-1)
-    return x + torch.sin(x * a).pow(2) / (a + getattr(snake, "no_div_by_zero", NO_DIV_BY_ZERO))
+def _kernel_input(x: torch.Tensor) -> torch.Tensor:
+    """The tensor the kernels take: a strided fp32 [B, C, T] CUDA tensor is copied
+    to a contiguous one; any other dtype, device or rank raises.  There is no
+    torch-expression path (the reference has one, server/kernels.py:110-112)."""
+    if not (x.is_cuda and x.dtype == torch.float32 and x.dim() == 3):
+        raise RuntimeError("contiguous fp32 CUDA BCT required")
+    return x if x.is_contiguous() else x.contiguous()
 
 
 def _fused_snake_forward(snake: torch.nn.Module, x: torch.Tensor) -> torch.Tensor:
-    if not _bct_ok(x):
-        return _snake_expr(snake, x)
+    x = _kernel_input(x)
     ops = load_snake_extension()
     bias = getattr(snake, "pre_bias", None)
     if bias is None:
@@ -204,15 +201,12 @@ def _fused_resblock_forward(block: torch.nn.Module, x: torch.Tensor) -> torch.Te
         y = block.activations2[i](y)
         y = block.convs2[i](y)
         bias = _residual_bias(block, i, y)
-        if _bct_ok(y) and _bct_ok(x):
-            ops = load_snake_extension()
-            if i + 1 < n:
-                x, pre = ops.residual_bias_snake(y, x, bias, _alpha(block.activations1[i + 1]))
-            else:
-                x, pre = ops.residual_bias(y, x, bias), None
+        y, x = _kernel_input(y), _kernel_input(x)
+        ops = load_snake_extension()
+        if i + 1 < n:
+            x, pre = ops.residual_bias_snake(y, x, bias, _alpha(block.activations1[i + 1]))
         else:
-            x = y + x + bias.to(y.dtype).unsqueeze(0).unsqueeze(-1)
-            pre = block.activations1[i + 1](x) if i + 1 < n else None
+            x, pre = ops.residual_bias(y, x, bias), None
     return x
 
 
@@ -229,11 +223,8 @@ def _fused_hift_decode(gen: torch.nn.Module, x: torch.Tensor, s: torch.Tensor) -
         if i == gen.num_upsamples - 1:
             x = gen.reflection_pad(x)
         x = x + gen.source_resblocks[i](gen.source_downs[i](s_stft))
-        outs = [gen.resblocks[i * nk + j](x) for j in range(nk)]
-        if nk == 3 and all(_bct_ok(o) for o in outs):
-            x = load_snake_extension().mean3(*outs)
-        else:
-            x = sum(outs) / nk
+        outs = [_kernel_input(gen.resblocks[i * nk + j](x)) for j in range(nk)]
+        x = load_snake_extension().mean3(*outs)
     x = gen.conv_post(F.leaky_relu(x))
     split = gen.istft_params["n_fft"] // 2 + 1
     wav = gen._istft(torch.exp(x[:, :split, :]), torch.sin(x[:, split:, :]))
@@ -244,6 +235,9 @@ def install_fused_snake(module: torch.nn.Module) -> int:
     """Route a HiFT generator's Snake / resblock / decode through the fused
     kernels (server/kernels.py:154-165); returns the number of Snake modules."""
     load_snake_extension()  # fail before the module is touched
+    if type(module).__name__ == "HiFTGenerator" and getattr(module, "num_kernels", 3) != 3:
+        # the fused decode averages the resblock branches with mean3
+        raise ValueError(f"install_fused_snake: HiFT decode needs 3 resblock kernels, got {module.num_kernels}")
     for block in [m for m in module.modules() if type(m).__name__ == "ResBlock"]:
         for i, (c1, c2, a2) in enumerate(zip(block.convs1, block.convs2, block.activations2)):
             if c1.bias is not None:
