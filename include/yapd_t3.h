@@ -5,7 +5,9 @@
  * hipStream_t passed as `void*` (NULL = the null stream).  Work is enqueued
  * on that stream and never synchronised; nothing here allocates device
  * memory or keeps hidden global state, so calls are re-entrant from one
- * host thread per stream.  Scratch memory is caller-owned ("workspace").
+ * host thread per stream.  Scratch memory is caller-owned ("workspace"),
+ * except in yapd_attn_paged_block_noalloc, whose split-KV partials live in a
+ * static device array per GPU (see there).
  *
  * Return value: YAPD_OK (0) or a nonzero YAPD_E* code; yapd_last_error()
  * then describes the failure (thread-local, valid until the next call).
@@ -118,6 +120,20 @@ int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, c
                           const int32_t* work, int n_work, const int32_t* merge, int n_merge,
                           const int32_t* counts, float* part_o, float* part_ml, int n_slots, float scale,
                           int causal, void* out, void* stream);
+
+/* Variant of yapd_attn_paged_block that allocates nothing and takes no
+ * workspace: the split-KV partials live in a file-scope device array of
+ * 16 MiB per GPU (n_slots * bl * n_heads * 66 floats must fit, else
+ * YAPD_EINVAL before any launch).  It has no counterpart in the reference;
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU race (use one stream per GPU or
+ * order the streams).  Results equal yapd_attn_paged_block's bit for bit. */
+int yapd_attn_paged_block_noalloc(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                                  int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl,
+                                  int n_heads, const int32_t* work, int n_work, const int32_t* merge, int n_merge,
+                                  const int32_t* counts, int n_slots, float scale, int causal, void* out,
+                                  void* stream);
 
 /* ------------------------------------------------------------------------ *
  * (b) bf16 MFMA projections (nn.Linear layout: C = A W^T, fp32 accumulate).

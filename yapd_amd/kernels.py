@@ -36,6 +36,9 @@ _SIGNATURES = {
     "yapd_attn_paged_block": (c_int, [
         c_void, c_void, c_i64, c_void, c_int, c_int, c_void, c_int, c_int, c_int, c_void, c_int, c_void, c_int,
         c_void, c_void, c_void, c_int, c_float, c_int, c_void, c_void]),
+    "yapd_attn_paged_block_noalloc": (c_int, [
+        c_void, c_void, c_i64, c_void, c_int, c_int, c_void, c_int, c_int, c_int, c_void, c_int, c_void, c_int,
+        c_void, c_int, c_float, c_int, c_void, c_void]),
     "yapd_kv_write": (c_int, [c_void, c_void, c_i64, c_i64, c_void, c_i64, c_void, c_int, c_int, c_void, c_int,
                               c_int, c_int, c_void]),
     "yapd_kv_gather": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_void]),
