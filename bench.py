@@ -76,7 +76,7 @@ def parse():
                     default="step")
     ap.add_argument("--requests", type=int, default=384, help="serve workload: number of requests")
     ap.add_argument("--kernel-sample", action="store_true",
-                    help="only run the dominant GEMM (bench shape) and a 1 GiB copy, for rocprofv3 --pmc")
+                    help="only run each kernel of the step at the bench shape x3 and a 1 GiB copy, for rocprofv3 --pmc")
     return ap.parse_args()
 
 
@@ -136,7 +136,7 @@ def main():
     dev = torch.device("cuda:0")
     Bp, bl, L = args.pairs, args.block, args.layers
     if args.kernel_sample and args.workload == "step":
-        kernel_sample(dev, 2 * Bp * bl)
+        kernel_sample(dev, Bp, bl)
         return
     if args.workload == "attn_stress":
         attn_stress(args, dev)
@@ -601,23 +601,72 @@ def quant_projections(args, dev):
                      "frac": round(tf4 / BF16_PEAK_TFLOPS, 4)}}), flush=True)
 
 
-def kernel_sample(dev, N):
-    """The dominant kernel at the bench shape plus a plain 1 GiB device copy (the
-    FETCH_SIZE / WRITE_SIZE calibration), three dispatches each."""
+def kernel_sample(dev, Bp, bl):
+    """Every kernel of the step at the bench shape, three dispatches each and in this order, for
+    rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE / MFMA counters per dispatch): gate/up + SiLU, QKV +
+    RoPE + KV write, o_proj + residual, down_proj + residual, RMSNorm, speech head (two launches
+    per call), paged attention over three layers' pools (each ~0.9 GB of K/V, so no dispatch finds
+    its pool in the 256 MB MALL), scoring on two alternating 268 MB logits sets, then a plain
+    1 GiB device copy (the counter calibration)."""
     from yapd_amd import kernels
+    from yapd_amd.engines.hip import HipEngine
+    from yapd_amd.paged import AttnPlan
+    from yapd_amd.scoring import BlockScorer
+    from yapd_amd.synthetic import MASK_ID, STOP_ID, make_t3, uniform_lengths
+    B, D, H, F, V = 2 * Bp, 1024, 16, 4096, 8194
+    N = B * bl
+    model = make_t3(n_layers=3, seed=0, device=dev)
+    lens = uniform_lengths(Bp, 150, 600, seed=1)
+    starts = lens + lens
+    eng = HipEngine(model, max(starts) + 2 * bl, torch.bfloat16, batch_size=B, page_table_seed=2)
     g = torch.Generator(device=dev).manual_seed(0)
-    A = torch.randn(N, 1024, generator=g, device=dev).bfloat16()
-    W = (torch.randn(8192, 1024, generator=g, device=dev) * 0.02).bfloat16()
-    act = torch.empty(N, 4096, dtype=torch.bfloat16, device=dev)
+    for pool in eng.kv.pools:
+        pool.copy_(torch.randn(pool.shape, generator=g, device=dev, dtype=torch.bfloat16))
+    buf = eng._buffers(B, bl)
+    buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+    normed = torch.randn(N, D, generator=g, device=dev).bfloat16()
+    attn_in = torch.randn(N, D, generator=g, device=dev).bfloat16()
+    act = torch.randn(N, F, generator=g, device=dev).bfloat16()
+    resid = torch.randn(N, D, generator=g, device=dev).bfloat16()
+    w = eng._w[0]
+    head_w = model.speech_head.weight.detach().contiguous()
+    ctx = torch.randn(B, 1, D, generator=g, device=dev).bfloat16()
+    logits_buf = torch.zeros(B, bl, (V + 7) // 8 * 8, dtype=torch.bfloat16, device=dev)
+    plan = AttnPlan([s + bl for s in starts], bl, H, dev)
+    q = torch.randn(B, bl, H, 64, generator=g, device=dev).bfloat16()
+    out = torch.empty_like(q)
+    sets = [(torch.randn(B, bl, (V + 7) // 8 * 8, generator=g, device=dev) * 3).bfloat16() for _ in range(2)]
+    log_prior = torch.log_softmax(torch.randn(V, generator=g, device=dev), 0)
+    scorer = BlockScorer(n_pairs=Bp, block_size=bl, log_prior=log_prior, mask_id=MASK_ID, stop_id=STOP_ID,
+                         num_steps=10, time_shift_tau=3.0, omnivoice_t_shift=0.5, cfg_scale=0.5, device=dev)
+    xt = torch.full((Bp, bl), MASK_ID, dtype=torch.int64, device=dev)
+    k_step = torch.zeros(Bp, dtype=torch.int64, device=dev)
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize(dev)
-    for _ in range(3):
-        kernels.gemm_swiglu(A, W, act)
-    for _ in range(3):
-        dst.copy_(src)
+    order = []
+
+    def run(label, fn, reps=3):
+        for i in range(reps):
+            fn(i)
+            order.append(label)
+    run("gate_up_swiglu", lambda i: kernels.gemm_swiglu(normed, w["wgu"], buf.act))
+    run("qkv_rope_kv", lambda i: kernels.gemm_qkv_rope_kv(normed, w["wqkv"], eng._cos, eng._sin, buf.pos0, bl, buf.q,
+                                                          eng.kv.pools[0], eng.kv.table))
+    run("o_proj_residual", lambda i: kernels.gemm_bf16_residual(attn_in, w["wo"], resid))
+    run("down_proj_residual", lambda i: kernels.gemm_bf16_residual(act, w["wd"], resid))
+    run("rmsnorm", lambda i: kernels.rmsnorm(resid, w["ln_in"], 1e-5, buf.normed))
+    run("speech_head", lambda i: kernels.gemm_head_shift(normed.view(B, bl, D), ctx, head_w,
+                                                         logits_buf[..., :V]))
+    run("attention", lambda i: plan.run(q, eng.kv.pools[i], eng.kv.table, out, 0.125))
+    run("scoring", lambda i: scorer(sets[i % 2][..., :V], xt, k_step, layout="stacked"))
+    run("copy_1GiB", lambda i: dst.copy_(src))
     torch.cuda.synchronize(dev)
-    print(json.dumps({"kernel_sample": "gemm_swiglu M=%d N=8192 K=1024 x3; copy %d bytes x3" % (N, COPY_BYTES)}))
+    kv_len = plan.kv_len_host
+    print(json.dumps({"kernel_sample": order, "M": N, "copy_bytes": COPY_BYTES,
+                      "attention_bytes": sum(kv_len) * H * 64 * 2 * 2 + 2 * N * H * 64 * 2
+                      + sum((k + 15) // 16 for k in kv_len) * 4,
+                      "scoring_bytes": B * bl * V * 2 + V * 4 + Bp * bl * 29 + Bp * 13}), flush=True)
 
 
 def host_cpu_info() -> dict:
