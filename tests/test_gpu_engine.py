@@ -196,3 +196,24 @@ def test_engine_rejects_bad_inputs(dev, one_layer):
     with pytest.raises(ValueError):
         eng.block_forward(torch.zeros(2, 16, 1024, dtype=torch.bfloat16, device=dev), 120)
     assert eng.can_reuse(100, torch.bfloat16, batch_size=2) and not eng.can_reuse(200, torch.bfloat16, batch_size=2)
+
+
+def test_recapture_at_another_block_size_keeps_the_prefix(dev, one_layer):
+    """capture_cuda_graph at bl = 16, then at bl = 32 with unchanged cache
+    starts: the second graph must be re-planned for the new block size (its
+    keys cover the prefix), so its replay equals the eager block forward."""
+    model = one_layer
+    B, lps = 2, [100, 140]
+    g = torch.Generator().manual_seed(6)
+    prefixes = [torch.randn(1, lp, 1024, generator=g).bfloat16().to(dev) for lp in lps]
+    eng = HipEngine(model, 512, torch.bfloat16, batch_size=B)
+    sos = eng.prefix_forward(prefixes)
+    for bl in (16, 32):
+        block = torch.randn(B, bl, 1024, generator=g).bfloat16().to(dev)
+        eng.capture_cuda_graph(bl, speech_head=model.speech_head)
+        eng.set_shift_ctx(sos)
+        assert eng._g_plan.kv_len.tolist() == [lp + bl for lp in lps]
+        hid_g, _ = eng.block_forward_graph(block, lps)
+        hid_g = hid_g.clone()
+        hid_e = eng.block_forward(block, lps)
+        assert torch.equal(hid_g, hid_e), f"bl={bl}"
