@@ -8,7 +8,11 @@
 //
 // Work decomposition: a workgroup of four waves serves one (row, key range)
 // work item for four heads, one head per wave, so a workgroup streams
-// 4 heads x (2 KiB K + 2 KiB V) contiguous bytes per page.  Per 32-key chunk a
+// 4 heads x (2 KiB K + 2 KiB V) contiguous bytes per page.  The H / 4
+// workgroups of one item are consecutive in the 1-D grid: they are dispatched
+// together and read the neighbouring 8 KiB runs of the same pages at about
+// the same time (measured 170 -> 164 us per layer at 512 rows x 32 against a
+// 2-D grid whose head groups of one item were a whole grid row apart).  Per 32-key chunk a
 // wave computes S^T = K Q^T (v_mfma_f32_16x16x32_bf16, M = keys, N = 16
 // queries) and O^T += V^T P^T (M = head dim, N = queries): with the
 // transposed products every lane owns one query, so the online-softmax
@@ -92,9 +96,11 @@ template <int NQT>
 __global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParams P) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * kWaves + wave;
-  if (P.counts != nullptr && static_cast<int>(blockIdx.x) >= P.counts[0]) return;
-  const int4 it = reinterpret_cast<const int4*>(P.work)[blockIdx.x];
+  const int hgroups = P.H / kWaves;
+  const int item = static_cast<int>(blockIdx.x) / hgroups;
+  const int h = (static_cast<int>(blockIdx.x) - item * hgroups) * kWaves + wave;
+  if (P.counts != nullptr && item >= P.counts[0]) return;
+  const int4 it = reinterpret_cast<const int4*>(P.work)[item];
   const int r = it.x, kb = it.y, ke = it.z, slot = it.w;
   const int kvl = P.kv_len[r];
   const int g = lane >> 4;   // lane group: key group / head-dim group
@@ -497,7 +503,7 @@ int attn_launch(const void* q, const void* kv_pool, int64_t n_pages, const int32
   P.causal = causal != 0;
   P.out = static_cast<uint16_t*>(out);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(n_work, n_heads / yapd::kWaves), block(64 * yapd::kWaves);
+  const dim3 grid(n_work * (n_heads / yapd::kWaves)), block(64 * yapd::kWaves);
   switch ((bl + 15) / 16) {
     case 1: hipLaunchKernelGGL(yapd::attn_paged_kernel<1>, grid, block, 0, st, P); break;
     case 2: hipLaunchKernelGGL(yapd::attn_paged_kernel<2>, grid, block, 0, st, P); break;
