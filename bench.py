@@ -30,7 +30,8 @@ over a queue of requests and reports committed speech tokens per second.
 
 ``--workload vocoder`` times the HiFT vocoder's elementwise family on the
 last-stage tensors of a 48-chunk micro-batch of 80-token chunks
-([48, 64, 19201] fp32) against the HBM roofline.
+([48, 64, 19201] fp32) against the HBM roofline, and the streaming
+vocoder's chunk stitch on a 48-job batch.
 
 ``--workload prefill`` times the prefix prefill of the step's rows (causal,
 64-token chunks through the paged KV) in prefix tokens per second.
@@ -475,6 +476,7 @@ def vocoder_workload(args, dev):
         ms = time_launches(fn, max(args.steps, 10), dev)
         res[name] = {"us": round(ms * 1e3, 1), "gbs": round(tensors * 4 * n / (ms * 1e-3) / 1e9, 1)}
         log(f"{name}: {ms * 1e3:.1f} us, {res[name]['gbs']:.0f} GB/s")
+    res["stitch"] = stitch_sample(args, dev, g)
     dom = res["residual_bias_snake"]
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "vocoder_residual_bias_snake_traffic.json")
@@ -503,6 +505,40 @@ def vocoder_workload(args, dev):
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "bytes_per_launch": 4 * 4 * n, "traffic": traffic},
         "kernels": res, "cpu_baseline": cpu}), flush=True)
+
+
+def stitch_sample(args, dev, g):
+    """Chunk stitching of the streaming vocoder (voc_stitch.hip) on a bulk micro-batch: 48 jobs,
+    96-token windows (16 tokens of lookback + 80 emitted), each blending a 480-sample tail and
+    withholding the next.  Bytes per job: the samples read (fp32), the tail read and written
+    (fp32) and the PCM written (int16).  Also times the batch's copy to pinned host memory as
+    int16 PCM against the fp32 waveforms a host-side stitch would copy."""
+    from yapd_amd import kernels as K
+    nj, ntok, emit_off, fade = 48, 96, 16, 480
+    wav = torch.randn(nj, ntok * 960, generator=g, device=dev) * 0.5
+    lo = emit_off * 960 - fade
+    n_seg = ntok * 960 - lo
+    n_out = n_seg - fade
+    jobs = torch.tensor([[i, lo, n_seg, fade, 0, 0, n_out, i, i, i * n_out, 0, 0] for i in range(nj)],
+                        dtype=torch.int32, device=dev)
+    fin = torch.linspace(0, 1, fade, device=dev)
+    fout = 1 - fin
+    trim = torch.ones(960, device=dev)
+    t_in = torch.randn(nj, fade, generator=g, device=dev)
+    t_out = torch.empty_like(t_in)
+    pcm = torch.empty(nj * n_out, dtype=torch.int16, device=dev)
+    ms = time_launches(lambda: K.voc_stitch(wav, jobs, fin, fout, trim, t_in, t_out, pcm), max(args.steps, 10), dev)
+    nbytes = nj * (4 * n_seg + 8 * fade + 2 * n_out)
+    pin16 = torch.empty(pcm.numel(), dtype=torch.int16, pin_memory=True)
+    pin32 = torch.empty(wav.shape, dtype=torch.float32, pin_memory=True)
+    ms16 = time_launches(lambda: pin16.copy_(pcm, non_blocking=True), 10, dev)
+    ms32 = time_launches(lambda: pin32.copy_(wav, non_blocking=True), 10, dev)
+    out = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes,
+           "jobs": nj, "samples_out": nj * n_out, "d2h_int16_us": round(ms16 * 1e3, 1),
+           "d2h_fp32_us": round(ms32 * 1e3, 1)}
+    log(f"stitch: {out['us']} us for {nj} jobs ({out['gbs']:.0f} GB/s); PCM to host {out['d2h_int16_us']} us "
+        f"as int16 vs {out['d2h_fp32_us']} us for the fp32 waveforms")
+    return out
 
 
 def serve(args, dev):

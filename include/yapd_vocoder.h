@@ -48,6 +48,37 @@ int yapd_branch_start(const float* x, const float* source, const float* alpha0, 
                       const float* alpha2, float* raw_out, float* out0, float* out1, float* out2, int64_t B, int C,
                       int64_t T, void* stream);
 
+/* Chunk stitching of the streaming vocoder for a whole micro-batch: replaces
+ * the per-job numpy post-processing of Vocoder._postprocess
+ * (server/vocoder.py:284-320) after the batch's HiFT pass (:271-279).
+ *
+ * wav: fp32 [rows][wav_stride] device array (the batch's waveforms, wav_cols
+ * valid samples per row).  jobs: device int32 [n_jobs][YAPD_STITCH_JOB_INTS],
+ * per job
+ *   0 row      batch row of the job
+ *   1 lo       first sample of the row the job uses
+ *   2 n_seg    samples used from lo on
+ *   3 n_blend  leading samples blended as tail * fade_out + x * fade_in with
+ *              tails_in[tail_in] (0: none)
+ *   4 trim     1: multiply the first min(n_trim, n_seg) samples by trim
+ *   5 pre_roll zeros placed before the samples
+ *   6 n_out    samples of the result written to pcm (pre_roll + n_seg, or
+ *              that minus fade when the job withholds a tail)
+ *   7 tail_in  row of tails_in for the blend (-1: none)
+ *   8 tail_out row of tails_out that receives the last fade samples of the
+ *              result, before clipping (-1: none)
+ *   9 pcm_off  first pcm sample of the job
+ *   10, 11     unused (0)
+ * pcm = trunc(clip(result, -1, 1) * 32767), every product and sum rounded
+ * separately as numpy does in float32.  A job that does not fit the buffers
+ * it names is skipped.  fade_in / fade_out: fade floats each; trim: n_trim
+ * floats. */
+#define YAPD_STITCH_JOB_INTS 12
+int yapd_voc_stitch(const float* wav, int64_t wav_stride, int64_t wav_cols, int rows, const int32_t* jobs,
+                    int n_jobs, const float* fade_in, const float* fade_out, int fade, const float* trim, int n_trim,
+                    const float* tails_in, int n_tails_in, float* tails_out, int n_tails_out, int16_t* pcm,
+                    int64_t pcm_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,6 +30,7 @@ COMMON_FLAGS = [
 # Files whose fp32 op order must follow the reference exactly (no FMA contraction).
 PER_FILE_FLAGS = {
     "score.hip": ["-ffp-contract=off"],
+    "voc_stitch.hip": ["-ffp-contract=off"],
 }
 
 

@@ -67,7 +67,11 @@ _SIGNATURES = {
                                          c_void]),
     "yapd_branch_start": (c_int, [c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_void, c_i64,
                                   c_int, c_i64, c_void]),
+    "yapd_voc_stitch": (c_int, [c_void, c_i64, c_i64, c_int, c_void, c_int, c_void, c_void, c_int, c_void, c_int,
+                                c_void, c_int, c_void, c_int, c_void, c_i64, c_void]),
 }
+
+STITCH_JOB_INTS = 12  # YAPD_STITCH_JOB_INTS of include/yapd_vocoder.h
 
 
 class T3Layer(ctypes.Structure):
@@ -480,3 +484,40 @@ def tick_update(*, xt: torch.Tensor, xt_blk: torch.Tensor, xt_new: torch.Tensor,
         xt_blk.data_ptr(), xt_new.data_ptr(), k_step.data_ptr(), cache_len.data_ptr(), blk_start.data_ptr(),
         is_commit.data_ptr(), n_speech.data_ptr(), hidden.data_ptr(), shift_ctx.data_ptr(), flags.data_ptr(),
         xt_final.data_ptr(), stream_ptr(dev)))
+
+
+# --------------------------------------------------------------------------- #
+# streaming vocoder: chunk stitching
+# --------------------------------------------------------------------------- #
+
+def voc_stitch(wav: torch.Tensor, jobs: torch.Tensor, fade_in: torch.Tensor, fade_out: torch.Tensor,
+               trim: torch.Tensor, tails_in: Optional[torch.Tensor], tails_out: Optional[torch.Tensor],
+               pcm: torch.Tensor) -> None:
+    """Stitch a micro-batch's chunks into int16 PCM (``yapd_voc_stitch``, include/yapd_vocoder.h).
+
+    ``wav`` fp32 ``[rows, S]`` with a unit last stride; ``jobs`` int32
+    ``[n_jobs, 12]`` on the device (the layout of the header); ``fade_in`` /
+    ``fade_out`` fp32 ``[fade]``; ``trim`` fp32 ``[n_trim]``; ``tails_in`` /
+    ``tails_out`` fp32 ``[n, fade]`` or None; ``pcm`` int16, flat.
+    """
+    lib = load_library()
+    dev = wav.device
+    require_cuda(wav, "wav", torch.float32, dev, contiguous=False)
+    require(wav.dim() == 2 and wav.stride(1) == 1, "wav must be [rows, samples] with unit last stride")
+    require_cuda(jobs, "jobs", torch.int32, dev)
+    require(jobs.dim() == 2 and jobs.shape[1] == STITCH_JOB_INTS, f"jobs must be [n, {STITCH_JOB_INTS}]")
+    fade = fade_in.numel()
+    for t, name in ((fade_in, "fade_in"), (fade_out, "fade_out"), (trim, "trim")):
+        require_cuda(t, name, torch.float32, dev)
+    require(fade_out.numel() == fade, "fade_in and fade_out must have the same length")
+    for t, name in ((tails_in, "tails_in"), (tails_out, "tails_out")):
+        if t is not None:
+            require_cuda(t, name, torch.float32, dev)
+            require(t.dim() == 2 and t.shape[1] == fade, f"{name} must be [n, {fade}]")
+    require_cuda(pcm, "pcm", torch.int16, dev)
+    n_in = 0 if tails_in is None else tails_in.shape[0]
+    n_out = 0 if tails_out is None else tails_out.shape[0]
+    check(lib.yapd_voc_stitch(wav.data_ptr(), wav.stride(0), wav.shape[1], wav.shape[0], jobs.data_ptr(),
+                              jobs.shape[0], fade_in.data_ptr(), fade_out.data_ptr(), fade, ptr(trim),
+                              trim.numel(), ptr(tails_in), n_in, ptr(tails_out), n_out, pcm.data_ptr(), pcm.numel(),
+                              stream_ptr(dev)))

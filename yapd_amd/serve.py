@@ -38,6 +38,7 @@ from .embed import SpeechEmbedder
 from .engines.hip import HipEngine
 from .paged import PAGE_SIZE
 from .scoring import BlockScorer
+from .voc_stream import maybe_vocode
 
 
 @dataclass
@@ -59,6 +60,14 @@ class Request:
     known_tick: int = 0
     committed: list = field(default_factory=list)
     t3_done: bool = False
+    # streaming audio (server/engine.py:56-57, 67-72, 77-80): sink(bytes | None), None = end of stream
+    sink: object = None
+    emitted_tok: int = 0      # committed tokens handed to the vocoder
+    voc_tail: object = None   # crossfade tail of the last chunk (device tensor)
+    first_chunk_sent: bool = False
+    finished: bool = False    # audio stream closed
+    t_first_pcm: float = 0.0
+    audio_samples: int = 0
     # metrics (perf_counter)
     t_recv: float = 0.0
     t_admit: float = 0.0
@@ -118,7 +127,9 @@ class HipFlashEngine:
                  num_steps: int = 10, temperature: float = 0.6, time_shift_tau: float = 0.1,
                  omnivoice_t_shift: float = 0.5, cfg_scale: float = 1.0, position_temperature: float = 5.0,
                  prefill_max: int = 16, block_size: int = 16, lag: int = 2, seed: int = 1234,
-                 page_table_seed: Optional[int] = None):
+                 page_table_seed: Optional[int] = None, vocoder=None):
+        """``vocoder``: a :class:`yapd_amd.voc_stream.Vocoder` (or None); committed tokens are
+        handed to it in chunks as they are read back (server/engine.py:211-258)."""
         if block_size % PAGE_SIZE and PAGE_SIZE % block_size:
             raise ValueError("block size must divide or be a multiple of the 16-token page")
         if lag < 1:
@@ -137,6 +148,7 @@ class HipFlashEngine:
         self.prefill_max = int(prefill_max)
         self.lag = int(lag)
         self.seed = int(seed)
+        self.vocoder = vocoder
         S, nb, BS = self.S, self.nb, self.BS
 
         self.eng = HipEngine(model, self.L, torch.bfloat16, batch_size=S * nb, page_table_seed=page_table_seed)
@@ -303,6 +315,8 @@ class HipFlashEngine:
         if add and not r.committed:
             r.t_first_commit = now
         r.committed.extend(add)
+        if self.vocoder is not None:
+            maybe_vocode(self.vocoder, r, final=False)
 
     def _finish(self, r: Request, now: float) -> None:
         r.t3_done = True
@@ -310,6 +324,8 @@ class HipFlashEngine:
         r.n_tokens = len(r.committed)
         self._free_slot(r)
         self.finished.append(r)
+        if self.vocoder is not None:
+            maybe_vocode(self.vocoder, r, final=True)
 
     def _free_slot(self, r: Request) -> None:
         """Swap-with-last compaction (server/engine.py:467-487); the KV follows its page-table rows."""

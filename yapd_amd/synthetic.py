@@ -208,3 +208,57 @@ def make_t3(*, n_layers: int = 30, hidden: int = 1024, heads: int = 16, ffn: int
             pos = LearnedPositions(max_positions, hidden, device=device, dtype=dtype)
             pos.emb.weight.copy_(normal((max_positions, hidden), 0.02))
     return SyntheticT3(tf, head, emb, pos).eval()
+
+
+class _TableFlow:
+    """Token -> "mel" stand-in: frames 2t and 2t + 1 carry token t's id in channel 0."""
+
+    def __init__(self, n_mels: int = 80):
+        self.n_mels = n_mels
+
+    def inference(self, *, token, token_len, prompt_token, prompt_token_len, prompt_feat, prompt_feat_len,
+                  embedding, finalize, n_timesteps, meanflow):
+        B, T = token.shape
+        mels = torch.zeros(B, self.n_mels, 2 * T, dtype=torch.float32, device=token.device)
+        mels[:, 0, :] = token.float().repeat_interleave(2, dim=1)
+        return mels, None
+
+
+class _TableHift:
+    """Mel -> waveform stand-in: each token's 960 samples are row `token` of a fixed table."""
+
+    def __init__(self, table: torch.Tensor):
+        self.table = table  # [V, 960] fp32
+
+    def inference(self, *, speech_feat, cache_source):
+        tok = speech_feat[:, 0, 0::2].long()  # [B, T]
+        B, T = tok.shape
+        return self.table.to(speech_feat.device)[tok].reshape(B, T * self.table.shape[1]), None
+
+
+class TableS3Gen:
+    """An S3Gen stand-in whose audio is position-local and exact: token t always yields the same
+    960 samples (a seeded table, amplitude up to ~1.2 so clipping is exercised), whatever its
+    neighbours.  Vocoding any window of a token sequence therefore gives exactly the slice of one
+    vocode of the whole sequence, which makes chunked streaming checkable against a one-shot
+    render.  ``trim_fade`` has the shape of S3Gen's (20 ms of zeros, then a 20 ms raised-cosine
+    ramp at 24 kHz)."""
+
+    def __init__(self, vocab: int = 6561, seed: int = 0, device: str = "cpu"):
+        g = torch.Generator().manual_seed(seed)
+        self.table = (torch.rand(vocab, 960, generator=g) * 2.4 - 1.2).to(device)
+        self.dtype = torch.float32
+        self.flow = _TableFlow()
+        self.mel2wav = _TableHift(self.table)
+        n = 480
+        ramp = (torch.cos(torch.linspace(math.pi, 0.0, n)) + 1) / 2
+        self.trim_fade = torch.cat([torch.zeros(n), ramp])
+
+    @staticmethod
+    def ref_dict() -> dict:
+        return dict(prompt_token=torch.zeros(1, 4, dtype=torch.long), prompt_token_len=torch.tensor([4]),
+                    prompt_feat=torch.zeros(1, 8, 80), embedding=torch.zeros(1, 192))
+
+    def render(self, tokens) -> np.ndarray:
+        """One vocode of the whole token sequence, fp32 numpy (what the table gives)."""
+        return self.table.cpu()[torch.as_tensor(list(tokens), dtype=torch.long)].reshape(-1).numpy()
