@@ -79,7 +79,8 @@ class Request:
 class _AsyncPlan:
     """Attention plan with fixed-capacity device buffers, refreshed every tick
     from pinned staging buffers (a ring, so a refresh never waits for the GPU).
-    The launch grid is the capacity; the kernels read the live counts."""
+    The launch grid is the capacity; the kernels read the live counts, and the
+    merge launch is left out of a tick whose plan splits no row."""
 
     def __init__(self, rows: int, bl: int, n_heads: int, device: torch.device, target_items: int, depth: int = 4):
         self.rows, self.bl, self.target = rows, bl, target_items
@@ -96,11 +97,13 @@ class _AsyncPlan:
                         torch.zeros(2, dtype=torch.int32).pin_memory()) for _ in range(depth)]
         self._events: List[Optional[torch.cuda.Event]] = [None] * depth
         self._next = 0
+        self.n_merge_live = 0  # split rows of the current plan (0: the merge launch is left out)
 
     def update(self, kv_upper: List[int]) -> None:
         work, merge, n_slots = kernels.attn_plan(kv_upper, target_items=self.target)
         if work.shape[0] > self.cap or merge.shape[0] > self.rows or n_slots > self.n_slots:
             raise RuntimeError("attention plan exceeds the engine's capacity")
+        self.n_merge_live = int(merge.shape[0])
         i = self._next
         self._next = (i + 1) % len(self._stage)
         if self._events[i] is not None:
@@ -273,7 +276,7 @@ class HipFlashEngine:
         buf.pos0.view(A, nb).copy_(self.cache_len[:A, None])
         torch.add(buf.pos0, BS, out=self.kv_dev[:R])
         self.eng._run(buf, self.plan, self.kv_dev[:R], head_w=self.head_w, shift_ctx=self.shift_ctx[:R],
-                      logits=self.logits[:R])
+                      logits=self.logits[:R], merge=self.plan.n_merge_live > 0)
         res = self.scorer(self.logits[:R], xt_blk, self.k_step[:A], layout="interleaved" if nb == 2 else "stacked",
                           temperature=self.temp, position_noise=self.posT > 0, seed=self.seed,
                           rng_offset=self.tick_id << 24, n_pairs=A)
