@@ -241,3 +241,122 @@ def test_engine_hands_committed_tokens_to_the_vocoder(dev):
             ref, _ = OV.postprocess(s3.render(r.committed), 0, True, True, None, fin, fout, trim)
             assert np.abs(got.astype(np.int32) - ref[: len(got)]).max() <= 1, r.rid
         assert r.audio_samples == len(got)
+
+
+class _HiftStandIn:
+    """A HiFT-shaped generator (fused Snake installed) as S3Gen's mel2wav: its waveform depends on
+    the neighbouring frames, so stitched chunks differ from a one-shot render; each of its samples
+    is repeated 15 times to give S3Gen's 480 samples per mel frame."""
+
+    def __init__(self, dev):
+        from test_gpu_vocoder import HiFTGenerator
+        from yapd_amd.vocoder import install_fused_snake
+        g = torch.Generator().manual_seed(12)
+        gen = HiFTGenerator(g)
+        for p in gen.parameters():
+            p.data.mul_(0.5)
+        self.gen = gen.to(dev).eval()
+        assert install_fused_snake(self.gen) == 48
+
+    def inference(self, *, speech_feat, cache_source):
+        B, _, T = speech_feat.shape
+        s = torch.zeros(B, 1, 32 * T, device=speech_feat.device)
+        return self.gen.decode(speech_feat, s).repeat_interleave(15, dim=-1), None
+
+
+class _MelTableFlow:
+    """Tokens -> mels from a fixed table (both frames of a token get its row)."""
+
+    def __init__(self, dev, vocab=512):
+        g = torch.Generator().manual_seed(13)
+        self.table = (torch.randn(vocab, 80, generator=g) * 0.5).to(dev)
+
+    def inference(self, *, token, **kw):
+        return self.table[token].repeat_interleave(2, dim=1).transpose(1, 2).contiguous(), None
+
+
+def test_worker_on_a_hift_shaped_generator(dev):
+    cfg = dict(chunk_first=12, chunk=40, lookback=16)
+    s3 = TableS3Gen(vocab=512, device=dev)
+    s3.flow, s3.mel2wav = _MelTableFlow(dev), _HiftStandIn(dev)
+    voc = Vocoder(s3, TableS3Gen.ref_dict(), dev, max_batch=6, first_max_batch=3, pre_roll=120, **cfg)
+    fin, fout = OV.fade_tables(480)
+    trim = s3.trim_fade.numpy()
+    checked = [0]
+    orig = voc._stitch
+
+    def stitch_checked(real, lens, wavs):
+        chain = {}
+        for j in real:
+            t = j.req.voc_tail
+            chain.setdefault(id(j.req), None if t is None else t.cpu().numpy())
+        pcm_host, spans, tails = orig(real, lens, wavs)
+        for i, (j, n, (off, cnt)) in enumerate(zip(real, lens, spans)):
+            ref, ref_tail = OV.postprocess(wavs[i, : n * 960].cpu().numpy(), j.emit_off, j.first, j.final,
+                                           chain[id(j.req)], fin, fout, trim, pre_roll=120)
+            chain[id(j.req)] = ref_tail
+            assert np.array_equal(pcm_host[off: off + cnt].numpy(), ref), (j.req.rid, i)
+            checked[0] += 1
+        return pcm_host, spans, tails
+
+    voc._stitch = stitch_checked
+    rng = np.random.default_rng(21)
+    reqs, plans = [], []
+    for rid in range(7):
+        n = int(rng.integers(5, 150))
+        toks = rng.integers(0, 512, n).tolist()
+        arrivals, left = [], n
+        while left:
+            arrivals.append(min(int(rng.integers(4, 30)), left))
+            left -= arrivals[-1]
+        reqs.append(Req(rid))
+        plans.append((toks, arrivals))
+    step = 0
+    while any(not r.t3_done for r in reqs):
+        for r, (toks, arr) in zip(reqs, plans):
+            if r.t3_done:
+                continue
+            if step < len(arr):
+                n0 = sum(arr[:step])
+                r.committed.extend(toks[n0: n0 + arr[step]])
+                maybe_vocode(voc, r, final=False)
+            else:
+                r.t3_done = True
+                maybe_vocode(voc, r, final=True)
+        drain(voc)
+        step += 1
+    drain(voc)
+    zeros = lambda window: np.zeros(len(window) * 960, np.float32)
+    for r, (toks, arr) in zip(reqs, plans):
+        want, _ = OV.stream_pcm(toks, arr, cfg, zeros, trim, pre_roll=120)
+        assert r.closed == 1 and len(r.pcm()) == len(want), r.rid
+        assert np.abs(r.pcm().astype(np.int32)).max() > 0
+    assert checked[0] >= len(reqs) * 2
+
+
+def test_stitch_skips_jobs_that_do_not_fit_their_buffers(dev):
+    from yapd_amd import kernels as K
+    wav = torch.rand(2, 4 * 960, device=dev) * 2 - 1
+    fin = torch.linspace(0, 1, 480, device=dev)
+    fout = 1 - fin
+    trim = torch.ones(960, device=dev)
+    t_in = torch.rand(1, 480, device=dev)
+    t_out = torch.full((1, 480), 7.0, device=dev)
+    pcm = torch.full((8000,), 12345, dtype=torch.int16, device=dev)
+    n = 4 * 960
+    jobs = torch.tensor([
+        [0, 0, n, 0, 0, 0, n, -1, -1, 0, 0, 0],            # valid: row 0 whole, no tail
+        [2, 0, n, 0, 0, 0, n, -1, -1, 0, 0, 0],            # row out of range
+        [1, 960, n, 0, 0, 0, n, -1, -1, 0, 0, 0],          # samples past the row
+        [1, 0, n, 0, 0, 0, n, -1, -1, 6000, 0, 0],         # PCM past the buffer
+        [1, 0, n, 480, 0, 0, n, 3, -1, 4000, 0, 0],        # blend from a missing tail
+        [1, 0, n, 0, 0, 0, n - 100, -1, 0, 4000, 0, 0],    # withheld samples != fade
+        [1, 0, n, 0, 0, 0, n - 480, -1, 5, 4000, 0, 0],    # tail row out of range
+    ], dtype=torch.int32, device=dev)
+    K.voc_stitch(wav, jobs, fin, fout, trim, t_in, t_out, pcm)
+    got = pcm.cpu().numpy()
+    ref = (np.clip(wav[0].cpu().numpy(), -1, 1) * np.float32(32767)).astype(np.int16)
+    assert np.array_equal(got[:n], ref)
+    assert np.all(got[n:] == 12345) and bool((t_out == 7.0).all())
+    with pytest.raises(ValueError, match="n_jobs"):
+        K.voc_stitch(wav, torch.zeros(70000, 12, dtype=torch.int32, device=dev), fin, fout, trim, None, None, pcm)
