@@ -97,6 +97,13 @@ REJECTS = [
     ("yapd_mean3", (P, P, P, P, 0, None), b"n must be >= 1"),
     ("yapd_residual_bias_snake", (P, P, P, None, P, P, 2, 64, 100, None), b"NULL pointer"),
     ("yapd_branch_start", (P, P, P, P, P, P, P, None, P, 2, 64, 100, None), b"NULL pointer"),
+    ("yapd_voc_stitch", (P, 960, 960, 2, P, 70000, P, P, 480, P, 960, None, 0, None, 0, P, 100, None),
+     b"n_jobs must be in [0, 65535]"),
+    ("yapd_voc_stitch", (P, 100, 960, 2, P, 3, P, P, 480, P, 960, None, 0, None, 0, P, 100, None), b"bad wav shape"),
+    ("yapd_voc_stitch", (P, 960, 960, 2, P, 3, P, None, 480, P, 960, None, 0, None, 0, P, 100, None),
+     b"both fade ramps"),
+    ("yapd_voc_stitch", (P, 960, 960, 2, P, 3, P, P, 480, P, 960, None, 2, None, 0, P, 100, None), b"NULL tails_in"),
+    ("yapd_voc_stitch", (P, 960, 960, 2, P, 3, P, P, 480, None, 960, None, 0, None, 0, P, 100, None), b"NULL trim"),
     ("yapd_mfma_peak_probe", (0, 10, 1, P, None), b"1 <= blocks"),
     ("yapd_hbm_read_probe", (P, 100, 8, P, None), b"multiple of 16"),
     ("yapd_hbm_read_probe", (P + 4, 1024, 8, P, None), b"16-byte aligned"),
