@@ -140,6 +140,11 @@ def test_graph_replay_with_and_without_split_rows(dev, one_layer, lps):
     hid_g, _ = eng.block_forward_graph(block, lps)
     assert (eng._g_plan.n_merge_live > 0) == (max(lps) + bl > 1024)
     assert torch.equal(hid_g.cpu(), hid)
+    for rep in range(2):  # more replays, with the eager forward (the program's own work) between them
+        assert torch.equal(eng.block_forward(block, lps).cpu(), hid), rep
+        torch.cuda.synchronize()
+        hid_g, _ = eng.block_forward_graph(block, lps)
+        assert torch.equal(hid_g.cpu(), hid), rep
 
 
 def test_thirty_layers_block_step(dev):

@@ -197,3 +197,23 @@ def test_step_replay_with_split_row_matches_eager(world):
     # back to the unsplit starts: the graph without the merge launch again
     step.set_cache_starts(list(w["lps"]))
     assert eng._g_plan.n_merge_live == 0
+
+
+def test_step_replays_repeat_with_eager_work_between(world):
+    """Three replays of the step graph with the eager step (the program's own work) and a device
+    synchronisation between them: every replay equals the eager result bit for bit."""
+    w = world
+    step, eng = w["step"], w["eng"]
+    starts = list(w["lps"])
+    step.set_cache_starts(starts)
+    for rep in range(3):
+        res = step.replay()
+        torch.cuda.synchronize()
+        hid_g = eng._buffers(ROWS, BL).hidden.view(ROWS, BL, -1).clone()
+        logits_g = eng._g_logits.clone()
+        out_g = {k: getattr(res, k).clone() for k in ("sampled", "pmi", "unmask", "xt", "n_mask_after", "hit_eos")}
+        hid_e, logits_e, res_e = eager_step(w, starts)
+        assert torch.equal(hid_g, hid_e), rep
+        assert torch.equal(logits_g, logits_e), rep
+        for k, v in out_g.items():
+            assert torch.equal(v, getattr(res_e, k)), (rep, k)
