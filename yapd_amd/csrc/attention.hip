@@ -92,8 +92,14 @@ __device__ __forceinline__ float sum_xor16_32(float v) {
   return b.x + b.y;
 }
 
+// Three and four query tiles (blocks of 33-64 queries, the 64-token prefill
+// chunks) are held to two waves per SIMD: without the bound the compiler
+// takes 222 VGPRs + 64 AGPRs for four tiles, one wave per SIMD (prefill
+// 294 -> 280 ms with the bound, no spills).  One and two tiles keep the
+// compiler's choice (three waves per SIMD measured slower for two tiles).
 template <int NQT>
-__global__ __launch_bounds__(64 * kWaves) void attn_paged_kernel(const AttnParams P) {
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(NQT >= 3 ? 2 : 1))) void
+attn_paged_kernel(const AttnParams P) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int hgroups = P.H / kWaves;
