@@ -92,13 +92,14 @@ __device__ __forceinline__ float sum_xor16_32(float v) {
   return b.x + b.y;
 }
 
-// Three and four query tiles (blocks of 33-64 queries, the 64-token prefill
-// chunks) are held to two waves per SIMD: without the bound the compiler
-// takes 222 VGPRs + 64 AGPRs for four tiles, one wave per SIMD (prefill
-// 294 -> 280 ms with the bound, no spills).  One and two tiles keep the
-// compiler's choice (three waves per SIMD measured slower for two tiles).
+// Occupancy by query tiles, measured (no spills at any of them): three and
+// four tiles (blocks of 33-64 queries, the 64-token prefill chunks) are held
+// to two waves per SIMD -- without the bound the compiler takes 222 VGPRs +
+// 64 AGPRs for four tiles, one wave per SIMD (prefill 294 -> 280 ms); one tile
+// (16-token blocks, serving) to four (three by default: 66.9 -> 64.6 us at 256
+// rows); two tiles keep the compiler's two (three measured 3.7 % slower).
 template <int NQT>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(NQT >= 3 ? 2 : 1))) void
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(NQT >= 3 ? 2 : NQT == 1 ? 4 : 1))) void
 attn_paged_kernel(const AttnParams P) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
