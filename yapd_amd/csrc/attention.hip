@@ -95,11 +95,13 @@ __device__ __forceinline__ float sum_xor16_32(float v) {
 // Occupancy by query tiles, measured (no spills at any of them): three and
 // four tiles (blocks of 33-64 queries, the 64-token prefill chunks) are held
 // to two waves per SIMD -- without the bound the compiler takes 222 VGPRs +
-// 64 AGPRs for four tiles, one wave per SIMD (prefill 294 -> 280 ms); one tile
-// (16-token blocks, serving) to four (three by default: 66.9 -> 64.6 us at 256
-// rows); two tiles keep the compiler's two (three measured 3.7 % slower).
+// 64 AGPRs for four tiles, one wave per SIMD (prefill 294 -> 280 ms).  One and
+// two tiles keep the compiler's three and two: one more wave per SIMD made
+// two tiles 3.7 % slower, and one tile 2 % faster on 256 rows of <= 540 keys
+// but 4.5 % slower on the 30-layer stress shape (prefixes up to 2048 keys):
+// more resident waves are more scattered page streams at once.
 template <int NQT>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(NQT >= 3 ? 2 : NQT == 1 ? 4 : 1))) void
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(NQT >= 3 ? 2 : 1))) void
 attn_paged_kernel(const AttnParams P) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
