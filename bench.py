@@ -205,6 +205,9 @@ def main():
     # o_proj / down_proj as the step runs them: with the residual add in the epilogue
     ms_o = time_launches(lambda: kernels.gemm_bf16_residual(buf.attn, eng._w[nxt()]["wo"], buf.delta), 20, dev)
     ms_down = time_launches(lambda: kernels.gemm_bf16_residual(buf.act, eng._w[nxt()]["wd"], buf.delta), 20, dev)
+    # the vendor library on the gate/up shape (hipBLASLt through F.linear, plain bf16 store, no SiLU):
+    # what the part gives a plain GEMM of this size, for context next to the fused kernel
+    ms_vendor = time_launches(lambda: torch.nn.functional.linear(buf.normed, eng._w[nxt()]["wgu"]), 20, dev)
     eager_plan = AttnPlan(plan.kv_len.tolist(), bl, H, dev)
     # four layers' pools in turn (each ~0.9 GB of K/V, so no replay finds its pool in the 256 MB MALL),
     # replayed as graphs like the step
@@ -236,6 +239,8 @@ def main():
     gbs_attn = attn_bytes / (ms_attn * 1e-3) / 1e9
     gbs_score = score_bytes / (ms_score * 1e-3) / 1e9
     proj_flops = 2.0 * N * D * (3 * H * 64 + H * 64 + 2 * F + F) * L + 2.0 * N * D * V
+    log(f"vendor plain GEMM on the gate/up shape (hipBLASLt): {ms_vendor*1e3:.1f} us "
+        f"({flops_swiglu / (ms_vendor * 1e-3) / 1e12:.0f} TF/s)")
     log(f"gate/up {ms_swiglu*1e3:.1f} us ({tf_swiglu:.0f} TF/s), qkv {ms_qkv*1e3:.1f}, o {ms_o*1e3:.1f}, "
         f"down {ms_down*1e3:.1f}, attn {ms_attn*1e3:.1f} us ({gbs_attn:.0f} GB/s), score {ms_score*1e3:.1f} us "
         f"({gbs_score:.0f} GB/s)")
@@ -276,7 +281,11 @@ def main():
                      "bound": "mfma", "achieved": round(tf_swiglu, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf_swiglu / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                      "peak_measured": round(peak_meas, 1), "frac_of_measured": round(tf_swiglu / peak_meas, 4),
-                     "peak_measured_constant_operands": round(peak_meas_const, 1)},
+                     "peak_measured_constant_operands": round(peak_meas_const, 1),
+                     "vendor_gemm": {"library": "hipBLASLt (torch F.linear), same shape, plain store without SiLU",
+                                     "us": round(ms_vendor * 1e3, 1),
+                                     "achieved": round(flops_swiglu / (ms_vendor * 1e-3) / 1e12, 1),
+                                     "frac": round(flops_swiglu / (ms_vendor * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}},
         "kernels": {
             "attention": {"us": round(ms_attn * 1e3, 1), "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4),
