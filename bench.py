@@ -15,8 +15,9 @@ Prints one JSON line.  ``value`` = speech tokens/s = pairs * block / step time.
 the published bf16 peak and, as ``peak_measured``, against the sustained MFMA
 rate of a register-only calibration kernel on random operands spread like the
 step's (``peak_measured_constant_operands``: the same kernel on few-bit
-constants, which draw less power and run faster); ``kernels`` adds attention and
-scoring against the HBM roofline.  Per-kernel durations come from HIP events
+constants, which draw less power and run faster) and, as ``vendor_gemm``, against
+hipBLASLt's plain GEMM of the same shape (torch ``F.linear``, no SiLU) timed in
+the same run; ``kernels`` adds attention and scoring against the HBM roofline.  Per-kernel durations come from HIP events
 on the stream the kernel runs on, right after the timed region: around single
 launches for the GEMMs, and around one graph replay of 20 back-to-back calls
 for attention and scoring (calls shorter than their host launch work),
