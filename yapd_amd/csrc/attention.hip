@@ -183,6 +183,13 @@ attn_paged_kernel(const AttnParams P) {
   // Chunk k0 + 32 is loaded while chunk k0 is multiplied.
   u32x4_t kf[2][2], vf[4], kn[2][2], vn[4];
   if (kb < ke) load_chunk(kb, kf, vf);
+  // The first chunk (and q) complete here, before the loop: with a load still
+  // pending on entry the compiler's wait at the loop's first MFMA is vmcnt(0),
+  // which would also wait for the next chunk's loads issued just before it.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) asm volatile("" ::"v"(kf[t][0]), "v"(kf[t][1]));
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) asm volatile("" ::"v"(vf[mt]));
   for (int k0 = kb; k0 < ke; k0 += kChunk) {
     if (k0 + kChunk < ke) load_chunk(k0 + kChunk, kn, vn);
     const bool tail = k0 + kChunk > kvl;
