@@ -162,6 +162,18 @@ int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, 
                           void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride,
                           int table_cols, void* stream);
 
+/* Input RMSNorm + QKV + NeoX RoPE + paged KV write on the residual stream
+ * (engines/flashinfer.py:992-1035: input_layernorm, then the projections, RoPE
+ * and the pool write): x [M, K] contiguous bf16 rows are normalised into the
+ * caller's workspace normed [M, K] (HF LlamaRMSNorm, as yapd_rmsnorm with x),
+ * then yapd_gemm_qkv_rope_kv runs on normed.  Two launches on `stream`; every
+ * argument of both is checked before the first (a rejected call launches
+ * nothing). */
+int yapd_gemm_rmsnorm_qkv_rope_kv(const void* x, const void* ln_w, float eps, void* normed, const void* W_qkv,
+                                  int M, int K, int n_heads, const float* cos_t, const float* sin_t, int max_pos,
+                                  const int32_t* pos0, int bl, void* q_out, void* kv_pool, int64_t n_pages,
+                                  const int32_t* page_table, int table_stride, int table_cols, void* stream);
+
 /* Fused gate/up + SiLU*up (engines/flashinfer.py:433-455): W rows are
  * [gate f..f+31; up f..f+31] for f = 0, 32, ...; act [M, F]. */
 int yapd_gemm_swiglu(const void* A, int64_t lda, const void* W_gu_interleaved, int M, int F, int K, void* act,

@@ -74,6 +74,12 @@ REJECTS = [
      b"bad positions / table shape"),
     ("yapd_gemm_qkv_rope_kv", (P, 1024, P, 64, 1024, 16, P + 4, P, 2048, P, 32, P, P, 64, P, 8, 8, None),
      b"cos/sin must be 16-byte aligned"),
+    ("yapd_gemm_rmsnorm_qkv_rope_kv", (P, None, 1e-5, P, P, 64, 1024, 16, P, P, 2048, P, 32, P, P, 64, P, 8, 8, None),
+     b"rmsnorm: NULL pointer"),
+    ("yapd_gemm_rmsnorm_qkv_rope_kv", (P, P, 1e-5, P, P, 64, 1000, 16, P, P, 2048, P, 32, P, P, 64, P, 8, 8, None),
+     b"D must be a multiple of 512"),
+    ("yapd_gemm_rmsnorm_qkv_rope_kv", (P, P, 1e-5, P, P, 48, 1024, 16, P, P, 2048, P, 32, P, P, 64, P, 8, 8, None),
+     b"bad positions / table shape"),
     ("yapd_rmsnorm", (None, None, P, P, 1e-5, 64, 1000, P, None), b"D must be a multiple of 512"),
     ("yapd_rmsnorm", (P, P, P, P, 1e-5, 64, 1024, P, None), b"not both"),
     ("yapd_rmsnorm", (None, None, P, P, 1e-5, 0, 1024, P, None), b"empty"),

@@ -131,6 +131,49 @@ def test_gemm_qkv_rope_kv(dev, rows, H):
     assert torch.count_nonzero(pool.cpu().float().abs().sum(-1)[~touched]) == 0
 
 
+def test_gemm_rmsnorm_qkv_rope_kv_equals_the_two_steps(dev):
+    """The composed entry point (input RMSNorm into a workspace, then QKV + RoPE + KV write) equals
+    yapd_rmsnorm followed by yapd_gemm_qkv_rope_kv bit for bit: normed rows, q and the whole pool."""
+    D, H, bl, rows = 1024, 16, 32, 40
+    M = rows * bl
+    x = rnd(M, D, seed=21).to(dev)
+    ln_w = (torch.rand(D, generator=torch.Generator().manual_seed(22)) + 0.5).bfloat16().to(dev)
+    Wqkv = rnd(3 * H * 64, D, std=0.02, seed=23).to(dev)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
+    fr = torch.outer(torch.arange(1024).float(), inv)
+    emb = torch.cat([fr, fr], -1)
+    cos_t, sin_t = emb.cos().bfloat16().float().to(dev), emb.sin().bfloat16().float().to(dev)
+    pos0 = torch.tensor(np.random.default_rng(3).integers(0, 700, rows), dtype=torch.int32, device=dev)
+    n_pages = rows * 48 + 16
+    table = torch.from_numpy(np.random.default_rng(4).permutation(n_pages)[: rows * 48].reshape(rows, 48)
+                             .astype(np.int32)).to(dev)
+    outs = []
+    for composed in (True, False):
+        normed = torch.zeros(M, D, dtype=torch.bfloat16, device=dev)
+        q_out = torch.zeros(M, H * 64, dtype=torch.bfloat16, device=dev)
+        pool = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
+        if composed:
+            kernels.gemm_rmsnorm_qkv_rope_kv(x, ln_w, 1e-5, normed, Wqkv, cos_t, sin_t, pos0, bl, q_out, pool, table)
+        else:
+            kernels.rmsnorm(x, ln_w, 1e-5, normed)
+            kernels.gemm_qkv_rope_kv(normed, Wqkv, cos_t, sin_t, pos0, bl, q_out, pool, table)
+        torch.cuda.synchronize()
+        outs.append((normed, q_out, pool))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert outs[0][1].abs().sum() > 0
+    # a call the QKV checks reject (M not a multiple of bl) launches nothing, not even the norm
+    normed = torch.full((M, D), 3.0, dtype=torch.bfloat16, device=dev)
+    lib = kernels.load_library()
+    rc = lib.yapd_gemm_rmsnorm_qkv_rope_kv(
+        x.data_ptr(), ln_w.data_ptr(), 1e-5, normed.data_ptr(), Wqkv.data_ptr(), M, D, H, cos_t.data_ptr(),
+        sin_t.data_ptr(), cos_t.shape[0], pos0.data_ptr(), 24, q_out.data_ptr(), pool.data_ptr(), n_pages,
+        table.data_ptr(), table.stride(0), table.shape[1], kernels.stream_ptr(dev))
+    torch.cuda.synchronize()
+    assert rc == 1 and b"bad positions" in lib.yapd_last_error()
+    assert bool((normed == 3.0).all())
+
+
 @pytest.mark.parametrize("with_delta", [False, True])
 @pytest.mark.parametrize("D", [1024, 512, 1536, 2048])  # one to four 512-wide chunks per row
 def test_rmsnorm(dev, with_delta, D):

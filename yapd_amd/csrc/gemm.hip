@@ -1235,17 +1235,19 @@ extern "C" int yapd_gemm_swiglu(const void* A, int64_t lda, const void* W_gu_int
   return yapd::launch_gemm<yapd::kEpiSwiglu, yapd::kAPlain>(p, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
-                                     const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int bl,
-                                     void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table,
-                                     int table_stride, int table_cols, void* stream) {
-  GemmParams p{};
+namespace yapd {
+namespace {
+// Parameters and argument checks of the QKV + RoPE + KV-write GEMM (nothing launched).
+int qkv_params(GemmParams& p, const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
+               const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int bl, void* q_out,
+               void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride, int table_cols) {
+  p = GemmParams{};
   p.A = static_cast<const uint16_t*>(A);
   p.lda = lda;
   p.W = static_cast<const uint16_t*>(W_qkv);
   p.ldw = K;
   p.M = M;
-  p.N = 3 * n_heads * yapd::kHeadDim;
+  p.N = 3 * n_heads * kHeadDim;
   p.K = K;
   p.cos_t = cos_t;
   p.sin_t = sin_t;
@@ -1259,29 +1261,68 @@ extern "C" int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_q
   p.table = page_table;
   p.table_stride = table_stride;
   p.table_cols = table_cols;
-  if (int rc = yapd::check_common(p)) return rc;
+  if (int rc = check_common(p)) return rc;
   YAPD_REQUIRE(cos_t && sin_t && pos0 && q_out && kv_pool && page_table, "gemm_qkv: NULL pointer");
-  YAPD_REQUIRE(yapd::al16(cos_t) && yapd::al16(sin_t) && (reinterpret_cast<uintptr_t>(q_out) & 7u) == 0 &&
+  YAPD_REQUIRE(al16(cos_t) && al16(sin_t) && (reinterpret_cast<uintptr_t>(q_out) & 7u) == 0 &&
                    (reinterpret_cast<uintptr_t>(kv_pool) & 7u) == 0,
                "gemm_qkv: cos/sin must be 16-byte aligned, q_out and kv_pool 8-byte aligned");
   YAPD_REQUIRE(max_pos >= 1 && bl >= 1 && M % bl == 0 && n_heads >= 1 && n_pages >= 1 && n_pages <= INT32_MAX &&
                    table_cols >= 1 && table_stride >= table_cols,
                "gemm_qkv: bad positions / table shape");
-  return yapd::launch_gemm<yapd::kEpiQkv, yapd::kAPlain>(p, static_cast<hipStream_t>(stream));
+  return YAPD_OK;
 }
 
-extern "C" int yapd_rmsnorm(const void* delta, void* residual, const void* x, const void* w, float eps, int M, int D,
-                            void* out, void* stream) {
+int rmsnorm_checks(const void* delta, const void* residual, const void* x, const void* w, int M, int D,
+                   const void* out) {
   YAPD_REQUIRE(w && out && M >= 1, "rmsnorm: NULL pointer or empty");
   YAPD_REQUIRE(D % 512 == 0 && D <= 2048, "rmsnorm: D must be a multiple of 512 and <= 2048 (got %d)", D);
   YAPD_REQUIRE(delta ? (residual != nullptr) : (x != nullptr), "rmsnorm: need (delta, residual) or x");
   YAPD_REQUIRE(!(delta && x), "rmsnorm: pass either delta (residual add) or x, not both");
-  yapd::NormParams p{static_cast<const uint16_t*>(delta), static_cast<uint16_t*>(residual),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps, M, D,
-                     static_cast<uint16_t*>(out)};
-  hipLaunchKernelGGL(yapd::rmsnorm_kernel, dim3((M + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  return YAPD_OK;
+}
+
+int rmsnorm_launch(const void* delta, void* residual, const void* x, const void* w, float eps, int M, int D,
+                   void* out, hipStream_t st) {
+  NormParams p{static_cast<const uint16_t*>(delta), static_cast<uint16_t*>(residual), static_cast<const uint16_t*>(x),
+               static_cast<const uint16_t*>(w), eps, M, D, static_cast<uint16_t*>(out)};
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((M + 3) / 4), dim3(256), 0, st, p);
   YAPD_LAUNCH_CHECK("rmsnorm_kernel launch");
   return YAPD_OK;
+}
+}  // namespace
+}  // namespace yapd
+
+extern "C" int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
+                                     const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int bl,
+                                     void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                                     int table_stride, int table_cols, void* stream) {
+  yapd::GemmParams p;
+  if (int rc = yapd::qkv_params(p, A, lda, W_qkv, M, K, n_heads, cos_t, sin_t, max_pos, pos0, bl, q_out, kv_pool,
+                                n_pages, page_table, table_stride, table_cols))
+    return rc;
+  return yapd::launch_gemm<yapd::kEpiQkv, yapd::kAPlain>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int yapd_gemm_rmsnorm_qkv_rope_kv(const void* x, const void* ln_w, float eps, void* normed,
+                                             const void* W_qkv, int M, int K, int n_heads, const float* cos_t,
+                                             const float* sin_t, int max_pos, const int32_t* pos0, int bl,
+                                             void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                                             int table_stride, int table_cols, void* stream) {
+  // Every argument of both launches is checked before the first one starts.
+  if (int rc = yapd::rmsnorm_checks(nullptr, nullptr, x, ln_w, M, K, normed)) return rc;
+  yapd::GemmParams p;
+  if (int rc = yapd::qkv_params(p, normed, K, W_qkv, M, K, n_heads, cos_t, sin_t, max_pos, pos0, bl, q_out, kv_pool,
+                                n_pages, page_table, table_stride, table_cols))
+    return rc;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (int rc = yapd::rmsnorm_launch(nullptr, nullptr, x, ln_w, eps, M, K, normed, st)) return rc;
+  return yapd::launch_gemm<yapd::kEpiQkv, yapd::kAPlain>(p, st);
+}
+
+extern "C" int yapd_rmsnorm(const void* delta, void* residual, const void* x, const void* w, float eps, int M, int D,
+                            void* out, void* stream) {
+  if (int rc = yapd::rmsnorm_checks(delta, residual, x, w, M, D, out)) return rc;
+  return yapd::rmsnorm_launch(delta, residual, x, w, eps, M, D, out, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int yapd_qgemm_affine(const void* A, int64_t lda, const uint32_t* w_packed, const void* scales,

@@ -50,6 +50,9 @@ _SIGNATURES = {
     "yapd_gemm_qkv_rope_kv": (c_int, [c_void, c_i64, c_void, c_int, c_int, c_int, c_void, c_void, c_int, c_void,
                                       c_int, c_void, c_void, c_i64, c_void, c_int, c_int, c_void]),
     "yapd_rmsnorm": (c_int, [c_void, c_void, c_void, c_void, c_float, c_int, c_int, c_void, c_void]),
+    "yapd_gemm_rmsnorm_qkv_rope_kv": (c_int, [c_void, c_void, c_float, c_void, c_void, c_int, c_int, c_int, c_void,
+                                              c_void, c_int, c_void, c_int, c_void, c_void, c_i64, c_void, c_int,
+                                              c_int, c_void]),
     "yapd_qgemm_affine": (c_int, [c_void, c_i64, c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_int,
                                   c_void, c_i64, c_void]),
     "yapd_mfma_peak_probe": (c_int, [c_int, c_int, c_int, c_void, c_void]),
@@ -410,6 +413,38 @@ def gemm_qkv_rope_kv(A: torch.Tensor, W_qkv: torch.Tensor, cos_t: torch.Tensor, 
         A.data_ptr(), A.stride(0), W_qkv.data_ptr(), M, K, H, cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0],
         pos0.data_ptr(), bl, q_out.data_ptr(), pool.data_ptr(), pool.shape[0], table.data_ptr(), table.stride(0),
         table.shape[1], stream_ptr(dev)))
+
+
+def gemm_rmsnorm_qkv_rope_kv(x: torch.Tensor, ln_w: torch.Tensor, eps: float, normed: torch.Tensor,
+                             W_qkv: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor, pos0: torch.Tensor,
+                             bl: int, q_out: torch.Tensor, pool: torch.Tensor, table: torch.Tensor) -> None:
+    """Input RMSNorm of the residual stream ``x [M, K]`` into ``normed`` (a caller workspace of the
+    same shape), then :func:`gemm_qkv_rope_kv` on it (``yapd_gemm_rmsnorm_qkv_rope_kv``)."""
+    dev = x.device
+    require_cuda(x, "x", torch.bfloat16, dev)
+    require(x.dim() == 2, "x must be [M, K]")
+    M, K = x.shape
+    require_cuda(ln_w, "ln_w", torch.bfloat16, dev)
+    require(ln_w.numel() == K, "ln_w must have K entries")
+    require_cuda(normed, "normed", torch.bfloat16, dev)
+    require(tuple(normed.shape) == (M, K), "normed must be [M, K]")
+    require_cuda(W_qkv, "W_qkv", torch.bfloat16, dev)
+    H = pool.shape[2]
+    require(tuple(W_qkv.shape) == (3 * H * 64, K), "W_qkv must be [3*H*64, K]")
+    require_cuda(cos_t, "cos_t", torch.float32, dev)
+    require_cuda(sin_t, "sin_t", torch.float32, dev)
+    require(cos_t.shape == sin_t.shape and cos_t.dim() == 2 and cos_t.shape[1] == 64, "cos/sin must be [P, 64]")
+    require_cuda(pos0, "pos0", torch.int32, dev)
+    require(M % bl == 0 and pos0.numel() == M // bl, "pos0 must have M / bl entries")
+    require_cuda(q_out, "q_out", torch.bfloat16, dev)
+    require(tuple(q_out.shape) in ((M, H * 64), (M // bl, bl, H, 64)), "q_out shape")
+    require_cuda(pool, "pool", torch.bfloat16, dev)
+    require_cuda(table, "table", torch.int32, dev, contiguous=False)
+    require(table.stride(1) == 1 and table.shape[0] >= M // bl, "table shape")
+    check(load_library().yapd_gemm_rmsnorm_qkv_rope_kv(
+        x.data_ptr(), ln_w.data_ptr(), float(eps), normed.data_ptr(), W_qkv.data_ptr(), M, K, H, cos_t.data_ptr(),
+        sin_t.data_ptr(), cos_t.shape[0], pos0.data_ptr(), bl, q_out.data_ptr(), pool.data_ptr(), pool.shape[0],
+        table.data_ptr(), table.stride(0), table.shape[1], stream_ptr(dev)))
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor,
