@@ -200,8 +200,8 @@ def test_rmsnorm(dev, with_delta, D):
 @pytest.mark.parametrize("epi", ["store", "residual", "swiglu", "qkv"])
 def test_rows_do_not_depend_on_batch_size(dev, epi):
     """A row is bit-identical whether it is computed in a large call (256 x 256
-    direct-load kernel), a mid-sized one (128 x 128 register-staged kernel) or
-    a small one (one-wave 64 x 64 direct-load kernel): all issue the same MFMA
+    direct-load tiles), a mid-sized one (128 x 128 direct-load tiles of 8 waves)
+    or a small one (one-wave 64 x 64 direct-load tiles): all issue the same MFMA
     over K in the same order.  Continuous batching relies on it -- a request's
     tokens must not depend on how many requests share its step.  The mid size
     per epilogue is one that selects the 128 x 128 kernel."""
