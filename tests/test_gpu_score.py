@@ -67,6 +67,47 @@ def settle_exact_ties(tok, ref, lc, lu, cfg, oracle):
     return oracle(sampled=tok)
 
 
+def settle_confidence_near_ties(res, ref, k_step, sched, q, *, K, tau, mask_id, stop_id, max_frac=0.05):
+    """The unmask rule ranks fp32 confidences and counts those at or above an interpolated quantile
+    (server/engine.py:563-584).  Kernel and oracle confidences agree only to rounding (their softmax
+    denominators are summed in different orders), so where two masked confidences of a pair, or a
+    confidence and the pair's quantile threshold, lie within that rounding of each other, the
+    decision can go either way in any implementation.  A model whose positions share one token
+    makes such near-ties common.  Where the kernel's and the oracle's decisions differ: the oracle's
+    rule run on the kernel's own confidences must reproduce the kernel's decisions exactly, every
+    differing pair must hold a near-tie no wider than twice its largest confidence difference, and
+    at most ``max_frac`` of the pairs may differ, and their confidences must agree with the oracle's to
+    the 2e-5 tolerance of ``assert_exact``.  Returns the oracle's decisions on the kernel's confidences."""
+    unm = res.unmask.cpu().bool()
+    if torch.equal(unm, ref["do_unmask"]):
+        return ref, 0
+    pmi_k = res.pmi.cpu().float()
+    rule = S.unmask_rule(pmi_k, ref["is_mask"], k_step, sched, q, K=K, tau=tau)
+    assert torch.equal(unm, rule["do_unmask"]), "kernel decisions differ from the rule on its own confidences"
+    pairs = (unm != ref["do_unmask"]).any(1).nonzero().flatten().tolist()
+    assert len(pairs) <= max(1, int(max_frac * unm.shape[0])), f"{len(pairs)} pairs decided differently"
+    for b in pairs:
+        mk = ref["is_mask"][b]
+        pr, pk = ref["pmi"][b][mk].double(), pmi_k[b][mk].double()
+        eps = (pr - pk).abs().max().item()
+        assert eps <= 2e-5 + 2e-5 * pr.abs().max().item(), f"pair {b}: confidences differ by {eps:.3g}"
+        srt = pr.sort().values
+        # distance to the threshold, leaving out the confidence it equals when the quantile index is
+        # whole (that comparison moves with it); exact ties show up in the adjacent gaps
+        d = (pr - ref["tau_k"][b].double()).abs()
+        d = d[d > 0]
+        gap = d.min().item() if d.numel() else float("inf")
+        if srt.numel() > 1:
+            gap = min(gap, (srt[1:] - srt[:-1]).min().item())
+        assert gap <= 2 * eps, f"pair {b}: decisions differ without a near-tie (gap {gap:.3g}, eps {eps:.3g})"
+    out = dict(ref)
+    out["do_unmask"] = rule["do_unmask"]
+    out["xt_new"] = torch.where(rule["do_unmask"], ref["sampled"], torch.where(ref["is_mask"], mask_id, out["xt_new"]))
+    out["n_mask_after"] = (out["xt_new"] == mask_id).sum(1)
+    out["hit_eos"] = (out["xt_new"] == stop_id).any(1)
+    return out, len(pairs)
+
+
 def assert_exact(res, ref):
     assert torch.equal(res.sampled.cpu(), ref["sampled"])
     torch.testing.assert_close(res.pmi.cpu(), ref["pmi"], rtol=2e-5, atol=2e-5)

@@ -14,7 +14,8 @@ Checked per replay:
         (max(2e-2, 1.5 x the bf16 oracle's own error) vs fp32);
   (iii) sampled tokens, unmask mask, new tokens, n_mask_after and hit_eos equal
         ``oracle.scoring.score_step`` run on the GPU's own logits, bit for bit
-        (exact ties of the guided score settled as in test_gpu_score.py);
+        (exact ties of the guided score, and confidences that tie to within
+        their fp32 rounding, settled as in test_gpu_score.py);
   (iv)  graph replay equals the eager path (``block_forward`` +
         ``gemm_head_shift`` + a separate ``BlockScorer``) bit for bit, once
         with cache starts that split no row (graph without the merge launch)
@@ -27,7 +28,7 @@ import torch
 from oracle import llama as OL
 from oracle import scoring as OS
 from oracle.schedule import omnivoice_unmask_schedule, quantile_fractions
-from test_gpu_score import settle_exact_ties
+from test_gpu_score import settle_confidence_near_ties, settle_exact_ties
 from yapd_amd import kernels
 from yapd_amd.engines.hip import HipEngine
 from yapd_amd.scoring import BlockScorer
@@ -115,11 +116,14 @@ def decisions_vs_oracle(res, logits, w):
                              stop_id=STOP_ID, sampled=sampled)
     ref = settle_exact_ties(res.sampled.cpu(), oracle(), lc, lu, W, oracle)
     assert torch.equal(res.sampled.cpu(), ref["sampled"])
+    torch.testing.assert_close(res.pmi.cpu(), ref["pmi"], rtol=2e-5, atol=2e-5)
+    ref, n_near = settle_confidence_near_ties(res, ref, ks, sched, q, K=K, tau=TAU, mask_id=MASK_ID,
+                                              stop_id=STOP_ID)
+    print(f"decisions: {n_near} of {PAIRS} pairs settled at confidence near-ties")
     assert torch.equal(res.unmask.cpu().bool(), ref["do_unmask"])
     assert torch.equal(res.xt.cpu(), ref["xt_new"])
     assert torch.equal(res.n_mask_after.cpu().long(), ref["n_mask_after"])
     assert torch.equal(res.hit_eos.cpu().bool(), ref["hit_eos"])
-    torch.testing.assert_close(res.pmi.cpu(), ref["pmi"], rtol=2e-5, atol=2e-5)
     return ref
 
 
