@@ -25,6 +25,10 @@ rotating inputs so that none is served from the 256 MB MALL.  ``cpu_baseline``
 times the oracle (torch on the host cores) on a bounded sample of the same
 step.
 
+``secondary`` (skipped with ``--no-secondary``) carries, from the same run,
+the headline figures of the prefill, serve and attention-stress workloads
+below (about 15 s more).
+
 ``--workload serve`` runs the continuous-batching engine (server defaults:
 128 slots, block 16, K = 10, temperature 0.6, position temperature 5, CFG 1)
 over a queue of requests and reports committed speech tokens per second.
@@ -74,6 +78,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="step workload: skip the prefill / serve / attention-stress figures")
     ap.add_argument("--workload", choices=["step", "attn_stress", "quant", "serve", "vocoder", "prefill"],
                     default="step")
     ap.add_argument("--requests", type=int, default=384, help="serve workload: number of requests")
@@ -141,13 +147,13 @@ def main():
         kernel_sample(dev, Bp, bl)
         return
     if args.workload == "attn_stress":
-        attn_stress(args, dev)
+        print(json.dumps(attn_stress(args, dev)), flush=True)
         return
     if args.workload == "quant":
         quant_projections(args, dev)
         return
     if args.workload == "serve":
-        serve(args, dev)
+        print(json.dumps(serve(args, dev)), flush=True)
         return
     if args.workload == "vocoder":
         vocoder_workload(args, dev)
@@ -252,6 +258,10 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
 
+    secondary = None
+    if not args.no_secondary:
+        secondary = secondary_workloads(args, dev, model, eng, prefixes, lps)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model, eng, lps, bl, sc_in, args.cpu_layers, L)
@@ -300,8 +310,38 @@ def main():
             "measured_read_GBps": round(read_gbs, 1),
         },
         "cpu_baseline": cpu,
+        "secondary": secondary,
     }
     print(json.dumps(out), flush=True)
+
+
+def secondary_workloads(args, dev, model, eng, prefixes, lps):
+    """The other workloads' headline figures, measured in the same run after the step: the prefix
+    prefill of the step's 512 rows (through the step's engine, rewriting the same KV), continuous
+    batching on the same model, and 30 layers of attention over the stress shape.  The full
+    objects come from ``--workload prefill | serve | attn_stress``."""
+    L, D = args.layers, 1024
+    embs = [p.to(dev) for p in prefixes + prefixes]
+    ms_pf, wall_pf = time_prefill(eng, embs, 2, dev)
+    tokens = sum(lps)
+    tf_pf = prefill_flops(lps, L, D) / (ms_pf * 1e-3) / 1e12
+    log(f"prefill: {tokens} prefix tokens, {ms_pf:.1f} ms, {tokens / (ms_pf * 1e-3):.0f} tokens/s, {tf_pf:.0f} TF/s")
+    del embs
+    sv = serve(args, dev, model)
+    torch.cuda.empty_cache()
+    st = attn_stress(args, dev)
+    torch.cuda.empty_cache()
+    return {
+        "prefill": {"value": round(tokens / (ms_pf * 1e-3), 1), "unit": "prefix tokens/s", "ms": round(ms_pf, 3),
+                    "wall_ms": round(wall_pf, 2), "prefix_tokens": tokens, "rows": len(lps), "layers": L,
+                    "achieved_tflops": round(tf_pf, 1), "frac": round(tf_pf / BF16_PEAK_TFLOPS, 4)},
+        "serve": {"value": sv["value"], "unit": sv["unit"], "requests": sv["config"]["requests"],
+                  "slots": sv["config"]["slots"], "block": sv["config"]["block"], "ticks": sv["ticks"],
+                  "ms_per_tick": sv["ms_per_tick"], "ttfc_s_median": sv["ttfc_s_median"], "wall_s": sv["wall_s"]},
+        "attn_stress": {"value": st["value"], "unit": st["unit"], "ms_30_layers": st["ms_per_step"],
+                        "frac": st["roofline"]["frac"], "sequences": st["config"]["sequences"],
+                        "block": st["config"]["block"], "layers": st["config"]["layers"]},
+    }
 
 
 COPY_BYTES = 1 << 30
@@ -370,7 +410,8 @@ def attn_stress(args, dev):
     byts = L * (sum(kv_len) * H * 64 * 2 * 2 + 2 * rows * bl * H * 64 * 2 + n_used * 4)
     gbs = byts / (ms * 1e-3) / 1e9
     log(f"attention stress: {L} layers {ms:.3f} ms, {gbs:.0f} GB/s")
-    print(json.dumps({
+    del pools, tables
+    return {
         "metric": "block attention HBM GB/s, 30 layers back to back (attention stress)", "value": round(gbs, 1),
         "unit": "GB/s", "n_gpus": 1, "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic (N(0,1) K/V/q, random distinct pages)",
@@ -378,7 +419,25 @@ def attn_stress(args, dev):
                    "prefix_len": "round(exp(U[ln64, ln2048]))", "pool_pages_per_layer": n_pages, "layers": L,
                    "kv_positions_per_layer": sum(kv_len)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": byts // L}}), flush=True)
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": byts // L}}
+
+
+def time_prefill(eng, embs, reps, dev):
+    """(device ms, wall ms) per ``eng.prefix_forward(embs)``, averaged over ``reps`` calls."""
+    torch.cuda.synchronize(dev)
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.time()
+    st.record()
+    for _ in range(reps):
+        eng.prefix_forward(embs)
+    en.record()
+    torch.cuda.synchronize(dev)
+    return st.elapsed_time(en) / reps, (time.time() - t0) * 1e3 / reps
+
+
+def prefill_flops(lps, L, D):
+    """Algorithmic flops of a prefill: the projections of every real prefix token plus causal attention."""
+    return 2.0 * sum(lps) * D * 16384 * L + sum(4.0 * 16 * 64 * lp * (lp + 1) / 2 for lp in lps) * L
 
 
 def prefill_workload(args, dev):
@@ -397,21 +456,11 @@ def prefill_workload(args, dev):
     g = torch.Generator().manual_seed(args.seed + 3)
     embs = [torch.randn(lp, D, generator=g).to(torch.bfloat16).to(dev) for lp in lps]
     eng.prefix_forward(embs)  # warm-up (plans, buffers)
-    torch.cuda.synchronize(dev)
-    reps = max(2, args.steps // 5)
-    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.time()
-    st.record()
-    for _ in range(reps):
-        eng.prefix_forward(embs)
-    en.record()
-    torch.cuda.synchronize(dev)
-    wall = (time.time() - t0) / reps
-    ms = st.elapsed_time(en) / reps
+    ms, wall = time_prefill(eng, embs, max(2, args.steps // 5), dev)
     tokens = sum(lps)
-    flops = 2.0 * tokens * D * 16384 * L + sum(4.0 * 16 * 64 * lp * (lp + 1) / 2 for lp in lps) * L
+    flops = prefill_flops(lps, L, D)
     tflops = flops / (ms * 1e-3) / 1e12
-    log(f"prefill: {len(lps)} rows, {tokens} prefix tokens, {ms:.1f} ms ({wall * 1e3:.1f} ms wall), "
+    log(f"prefill: {len(lps)} rows, {tokens} prefix tokens, {ms:.1f} ms ({wall:.1f} ms wall), "
         f"{tokens / (ms * 1e-3):.0f} tokens/s, {tflops:.0f} TF/s")
     cpu = None
     if not args.no_cpu_baseline:
@@ -436,7 +485,7 @@ def prefill_workload(args, dev):
         "dtype": "bf16", "data": "synthetic (seeded random-init T3 weights, N(0,1) prefix embeddings)",
         "config": {"workload": "prefix prefill (causal 64-token chunks, paged KV)", "rows": len(lps),
                    "prefix_len": "U[150,600] per pair", "layers": L, "prefix_tokens": tokens,
-                   "wall_ms": round(wall * 1e3, 2)},
+                   "wall_ms": round(wall, 2)},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_prefill": flops, "traffic": None},
         "cpu_baseline": cpu}), flush=True)
@@ -551,15 +600,17 @@ def stitch_sample(args, dev, g):
     return out
 
 
-def serve(args, dev):
+def serve(args, dev, model=None):
     """Continuous batching (server/engine.py FlashEngine defaults): 128 slots, block 16,
     K = 10 denoise steps, temperature 0.6, position temperature 5.0, CFG 1.0, tau 0.1;
     requests with prefixes U[100, 300] and speech budgets of 208 tokens (13 blocks)
-    arrive all at once; the timed window runs from the first tick to the last commit."""
+    arrive all at once; the timed window runs from the first tick to the last commit.
+    ``model`` (the same seeded T3) is built when not given."""
     from yapd_amd.serve import HipFlashEngine, Request
     from yapd_amd.synthetic import MASK_ID, SOS_ID, STOP_ID, make_t3, uniform_lengths
     L, n_req, n_speech = args.layers, args.requests, 208
-    model = make_t3(n_layers=L, seed=args.seed, device=dev)
+    if model is None:
+        model = make_t3(n_layers=L, seed=args.seed, device=dev)
     V = model.speech_head.weight.shape[0]
     g = torch.Generator().manual_seed(args.seed + 1)
     prior = torch.distributions.Dirichlet(torch.full((V,), 0.1)).sample()
@@ -595,7 +646,7 @@ def serve(args, dev):
     ttfc = sorted(r.t_first_commit - r.t_recv for r in done if r.t_first_commit > 0)
     log(f"serve: {len(done)} requests, {toks} committed tokens in {secs:.2f} s over {ticks} ticks "
         f"({secs / max(ticks, 1) * 1e3:.2f} ms/tick)")
-    print(json.dumps({
+    return {
         "metric": "committed speech tokens/sec, continuous batching (128 slots, 30 layers)",
         "value": round(toks / secs, 1), "unit": "committed speech tokens/s", "n_gpus": 1,
         "higher_is_better": True, "dtype": "bf16",
@@ -606,7 +657,7 @@ def serve(args, dev):
                    "position_temperature": 5.0, "cfg_w": 1.0},
         "ticks": ticks, "ms_per_tick": round(secs / max(ticks, 1) * 1e3, 3),
         "ttfc_s_median": round(ttfc[len(ttfc) // 2], 3) if ttfc else None,
-        "commit_blocks": eng.commit_blocks}), flush=True)
+        "commit_blocks": eng.commit_blocks, "wall_s": round(secs, 3)}
 
 
 def quant_projections(args, dev):
