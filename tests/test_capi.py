@@ -31,6 +31,19 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_library_exports_only_the_declared_c_abi():
+    """The dynamic symbol table holds the declared yapd_* functions and no internal C++ helper."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    lib_path = kernels.load_library()._name
+    out = subprocess.run([nm, "-D", "--defined-only", lib_path], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert exported == set(declared_functions()), sorted(exported ^ set(declared_functions()))
+
+
 def test_ctypes_signatures_cover_header():
     assert set(declared_functions()) <= set(kernels._SIGNATURES)
 
