@@ -200,52 +200,56 @@ def test_rmsnorm(dev, with_delta, D):
 @pytest.mark.parametrize("epi", ["store", "residual", "swiglu", "qkv"])
 def test_rows_do_not_depend_on_batch_size(dev, epi):
     """A row is bit-identical whether it is computed in a large call (256 x 256
-    direct-load tiles), a mid-sized one (128 x 128 direct-load tiles of 8 waves)
-    or a small one (one-wave 64 x 64 direct-load tiles): all issue the same MFMA
-    over K in the same order.  Continuous batching relies on it -- a request's
-    tokens must not depend on how many requests share its step.  The mid size
-    per epilogue is one that selects the 128 x 128 kernel."""
+    direct-load tiles), a mid-sized one (128 x 128 direct-load tiles of 8 waves,
+    three LDS stages when the grid has at most one tile per CU, else two) or a
+    small one (one-wave 64 x 64 direct-load tiles): all issue the same MFMA over
+    K in the same order.  Continuous batching relies on it -- a request's tokens
+    must not depend on how many requests share its step.  The two mid sizes per
+    epilogue select the 128 x 128 kernel with three and with two stages; every
+    row of each call is compared with the large call."""
     H, D, bl = 16, 1024, 32
     big, small = 16384, 96
-    mid = {"store": 4096, "residual": 4096, "swiglu": 1024, "qkv": 2048}[epi]
+    mids = {"store": (4096, 6144), "residual": (4096, 6144), "swiglu": (512, 1024), "qkv": (1024, 2048)}[epi]
+    sizes = (big, *mids, small)
     A = rnd(big, D, seed=31).to(dev)
     if epi in ("store", "residual", "swiglu"):
         N = 8192 if epi == "swiglu" else 1024
         W = rnd(N, D, std=0.02, seed=32).to(dev)
+        R = rnd(big, N, seed=33).to(dev)
         outs = []
-        for M in (big, mid, small):
+        for M in sizes:
             if epi == "store":
                 C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
                 kernels.gemm_bf16(A[:M], W, C)
             elif epi == "residual":
-                C = rnd(M, N, seed=33).to(dev)
+                C = R[:M].clone()
                 kernels.gemm_bf16_residual(A[:M], W, C)
             else:
                 C = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
                 kernels.gemm_swiglu(A[:M], W, C)
-            outs.append(C[:small].cpu())
-        assert torch.equal(outs[0], outs[1])
-        assert torch.equal(outs[0], outs[2])
+            outs.append(C.cpu())
+        for M, out in zip(sizes[1:], outs[1:]):
+            assert torch.equal(outs[0][:M], out), M
         return
     Wqkv = rnd(3 * H * 64, D, std=0.02, seed=34).to(dev)
     inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
     fr = torch.outer(torch.arange(1024).float(), inv)
     emb = torch.cat([fr, fr], -1)
     cos_t, sin_t = emb.cos().bfloat16().float().to(dev), emb.sin().bfloat16().float().to(dev)
-    rows_big, rows_small = big // bl, small // bl
+    rows_big = big // bl
     pos0 = torch.from_numpy(np.random.default_rng(5).integers(0, 700, rows_big).astype(np.int32)).to(dev)
     n_pages = rows_big * 48
     table = torch.from_numpy(np.random.default_rng(6).permutation(n_pages).reshape(rows_big, 48).astype(np.int32)).to(dev)
     res = []
-    for M in (big, mid, small):
+    for M in sizes:
         pool = torch.zeros(n_pages, 2, H, 1024, dtype=torch.bfloat16, device=dev)
         q_out = torch.empty(M, H * 64, dtype=torch.bfloat16, device=dev)
         kernels.gemm_qkv_rope_kv(A[:M], Wqkv, cos_t, sin_t, pos0[: M // bl], bl, q_out, pool, table[: M // bl])
-        pages = table[:rows_small].reshape(-1).long()
-        res.append((q_out[:small].cpu(), pool[pages].cpu()))
-    for r in res[1:]:
-        assert torch.equal(res[0][0], r[0])
-        assert torch.equal(res[0][1], r[1])
+        res.append((q_out.cpu(), pool))
+    for M, (q, pool) in zip(sizes[1:], res[1:]):
+        pages = table[: M // bl].reshape(-1).long()
+        assert torch.equal(res[0][0][:M], q), M
+        assert torch.equal(res[0][1][pages].cpu(), pool[pages].cpu()), M
 
 
 def test_narrow_last_column_tile_is_split_bit_identically(dev):

@@ -620,7 +620,7 @@ template <class T, int NS>
 struct DlLayout {
   static_assert(T::BK == 64, "direct-load tiles use 128-byte LDS rows");
   static constexpr int WAVES = T::THREADS / 64;
-  static_assert(NS == 2 || (WAVES == 1 && NS >= 2 && NS <= 4), "more than two stages need a one-wave tile");
+  static_assert(NS >= 2 && NS <= 4, "two to four LDS stages");
   static constexpr int ROWB = 128;
   static constexpr int CPR = 8;  // 16-byte chunks per row
   static constexpr int RPI = 8;  // rows per 1 KB load instruction
@@ -642,6 +642,15 @@ struct DlLayout {
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Hand-off of an LDS stage across the workgroup: this wave's loads up to the
+// stage have landed (at most N later loads still in flight), its LDS reads
+// have completed (so the stage it read last may be overwritten), then the
+// workgroup barrier.  __syncthreads would also drain the later tiles' loads.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // 16 bytes per lane from src into LDS at lds_run + 16 * lane (lds_run must be
@@ -745,10 +754,10 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
   // NS LDS stages, NS - 1 tiles in flight.  Tile kt+NS-1 is requested at the
   // top of tile kt into the stage tile kt-1 used: its last fragments were
   // consumed by the MFMAs that ended tile kt-1.  Before the first fragments
-  // of tile kt+1 are read, the wave waits for its loads of that tile.  With
-  // several waves the barrier (whose fence drains vmcnt) also covers the
-  // other waves' loads; a one-wave tile waits on its own vmcnt and keeps the
-  // later tiles in flight.
+  // of tile kt+1 are read, the wave waits for its loads of that tile and
+  // keeps the later tiles in flight; with several waves a barrier then covers
+  // the other waves' loads of it (with two stages nothing later is in flight
+  // and __syncthreads does both).
   const int kt_n = p.K / T::BK;
 #pragma unroll
   for (int s = 0; s + 1 < NS; ++s)
@@ -756,15 +765,27 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
   const RowMeta rm = EPI == kEpiQkv ? qkv_row_meta<T>(p, m0, tid) : RowMeta{0, 0};
   // Tiles issued after tile t, when the fragments of tile t are first read.
   auto wait_tile = [&](int t) {
-    if constexpr (L::WAVES > 1) {
-      __syncthreads();
-    } else if constexpr (NS == 2) {
-      wait_vmcnt<0>();
-    } else {
-      if (min(t + NS - 2, kt_n - 1) - t == NS - 2) {
-        wait_vmcnt<(NS - 2) * L::LPT>();
+    if constexpr (NS == 2) {
+      if constexpr (L::WAVES > 1) {
+        __syncthreads();
       } else {
         wait_vmcnt<0>();
+      }
+    } else {
+      // the same condition in every wave: all of them take the same barriers
+      const bool full = min(t + NS - 2, kt_n - 1) - t == NS - 2;
+      if constexpr (L::WAVES > 1) {
+        if (full) {
+          stage_barrier<(NS - 2) * L::LPT>();
+        } else {
+          stage_barrier<0>();
+        }
+      } else {
+        if (full) {
+          wait_vmcnt<(NS - 2) * L::LPT>();
+        } else {
+          wait_vmcnt<0>();
+        }
       }
     }
   };
@@ -1142,10 +1163,18 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   // (measured against the register-staged 128 x 128 kernel, same session,
   // bit-identical: o 18.5 -> 16.9 us and down 53.4 -> 50.4 us at M = 4096,
   // down 72.9 -> 62.5 us at M = 6144); the quantised path keeps the
-  // register-staged kernel, which dequantises W on its way into LDS.
+  // register-staged kernel, which dequantises W on its way into LDS.  With at
+  // most one tile per CU a k-tile is too short to cover the load latency, so
+  // three stages keep two tiles in flight (o 16.8 -> 14.3-14.9 us, down
+  // 50.3-51.1 -> 41.0-42.9 us at M = 2304-4096, bit-identical); with more
+  // tiles two stages let two workgroups share a CU, which measured faster
+  // (down 61 vs 83 us at M = 6144).
   const int64_t small_tiles = static_cast<int64_t>((p.M + 127) / 128) * ((p.N + 127) / 128);
   p.xcd_band = small_tiles <= cu_count() ? 1 : 0;
-  if constexpr (BQ == 0) return launch_dl<TileM, EPI, AM>(p, st);
+  if constexpr (BQ == 0) {
+    if (small_tiles <= cu_count()) return launch_dl<TileM, EPI, AM, 3>(p, st);
+    return launch_dl<TileM, EPI, AM>(p, st);
+  }
   return launch_tile<TileS, EPI, AM, BQ>(p, st);
 }
 
