@@ -36,3 +36,20 @@ def test_quant_linear_module(dev):
     assert y.shape == (4, 64, 1024)
     rel = ((y.float() - x.float() @ w.T).abs().max() / (x.float() @ w.T).abs().max()).item()
     assert rel <= 2e-2  # 8-bit codes: quantisation error of W itself
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quant_rows_do_not_depend_on_batch_size(dev, bits):
+    """Every row of a quantised projection is bit-identical whichever of the three kernels computes
+    it -- direct-load 256 x 256 tiles (M = 16384), register-staged 128 x 128 tiles (M = 8192: two
+    tiles per CU), direct-load 128 x 128 tiles (M = 1024 and 96: at most one tile per CU, 4-bit
+    codes read as 8-byte chunks) -- since all dequantise W the same way and take the same MFMA
+    over K in the same order."""
+    N, K = 1000, 4096  # a partial last column tile
+    g = torch.Generator().manual_seed(50 + bits)
+    w = torch.randn(N, K, generator=g) * 0.02
+    A = torch.randn(16384, K, generator=g).bfloat16().to(dev)
+    packed, s, b = quantize_affine(w.to(dev), bits)
+    outs = [qgemm_affine(A[:M], packed, s, b, bits).cpu() for M in (16384, 8192, 1024, 96)]
+    for M, out in zip((8192, 1024, 96), outs[1:]):
+        assert torch.equal(outs[0][:M], out), M

@@ -818,8 +818,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
 
 // Affine-quantised W on the direct-load layout: A moves global -> LDS by
 // direct loads as in gemm_dl_kernel; W's codes (one 16-byte chunk per code
-// row and k-half or quarter), scales and biases come into registers one
-// k-tile ahead, and after the k-tile's MFMAs each thread dequantises its
+// row and k-half or quarter -- 8-byte chunks where 16-byte ones would not
+// give every thread one: 4-bit codes on 128-column tiles), scales and biases
+// come into registers one k-tile ahead, and after the k-tile's MFMAs each thread dequantises its
 // chunk (w = scale * q + bias, rounded once to bf16, as in gemm_kernel) and
 // writes it into the next stage's B tile in the same swizzled layout, so the
 // fragment reads and the MFMA loop are gemm_dl_kernel's.  Only W passes
@@ -849,12 +850,14 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
     for (int j = 0; j < L::LA; ++j) load_lds16(a_src[j] + kt * T::BK, a_dst + j * 1024);
   };
 
-  // W codes: a 16-byte chunk holds QVALS codes of one row; a row's k-tile (one
-  // quantisation group of 64) is QCH chunks; each thread owns CQ chunks.
-  constexpr int QVALS = 128 / BQ;
+  // W codes: a chunk of QB bytes holds QVALS codes of one row; a row's k-tile
+  // (one quantisation group of 64) is QCH chunks; each thread owns CQ chunks.
+  constexpr int QB = (T::BN * (T::BK * BQ / 128)) % T::THREADS == 0 ? 16 : 8;
+  constexpr int QW = QB / 4;  // 32-bit words per chunk
+  constexpr int QVALS = QB * 8 / BQ;
   constexpr int QCH = T::BK / QVALS;
   constexpr int CQ = T::BN * QCH / T::THREADS;
-  static_assert(CQ * T::THREADS == T::BN * QCH, "quantised tile loads must divide evenly");
+  static_assert(CQ >= 1 && CQ * T::THREADS == T::BN * QCH, "quantised tile loads must divide evenly");
   const uint32_t* q_src[CQ];
   const uint16_t* s_src[CQ];
   const uint16_t* z_src[CQ];
@@ -870,12 +873,21 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
     s_src[c] = p.qscale + n * (p.K / 64);
     z_src[c] = p.qbias + n * (p.K / 64);
   }
-  u32x4_t rq[CQ];
+  uint32_t rq[CQ][QW];
   uint16_t rs[CQ], rz[CQ];
   auto fetch_w = [&](int kt) {
 #pragma unroll
     for (int c = 0; c < CQ; ++c) {
-      rq[c] = *reinterpret_cast<const u32x4_t*>(q_src[c] + kt * T::BK * BQ / 32);
+      const uint32_t* src = q_src[c] + kt * T::BK * BQ / 32;
+      if constexpr (QW == 4) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) rq[c][w] = v[w];
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        rq[c][0] = v.x;
+        rq[c][1] = v.y;
+      }
       rs[c] = s_src[c][kt];
       rz[c] = z_src[c][kt];
     }
@@ -1174,8 +1186,14 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   if constexpr (BQ == 0) {
     if (small_tiles <= cu_count()) return launch_dl<TileM, EPI, AM, 3>(p, st);
     return launch_dl<TileM, EPI, AM>(p, st);
+  } else {
+    // Quantised W: the direct-load kernel on 128 x 128 tiles while the grid
+    // has at most one tile per CU (M = 256-4096, bit-identical: down 4-bit
+    // 58.1 -> 44.7 us at M = 256, 78.0 -> 72.5 us at M = 4096); larger grids
+    // keep the register-staged kernel (o at M = 8192: 29.3 vs 32.5 us).
+    if (small_tiles <= cu_count()) return launch_dlq<TileM, AM, BQ>(p, st);
+    return launch_tile<TileS, EPI, AM, BQ>(p, st);
   }
-  return launch_tile<TileS, EPI, AM, BQ>(p, st);
 }
 
 int check_common(const GemmParams& p) {
