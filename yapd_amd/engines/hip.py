@@ -29,7 +29,7 @@ import torch
 from torch import Tensor
 
 from .. import kernels
-from ..paged import PAGE_SIZE, AttnPlan, PagedKV
+from ..paged import PAGE_SIZE, AttnPlan, PagedKV, to_device_async
 
 logger = logging.getLogger(__name__)
 
@@ -327,7 +327,7 @@ class HipEngine:
             if na == n:
                 buf.emb.view(n, bl, D).copy_(padded[:, c0: c0 + bl])
             else:
-                idx = torch.tensor(active, dtype=torch.long, device=dev)
+                idx = to_device_async(active, torch.long, dev)
                 buf.emb.view(na, bl, D).copy_(padded[idx, c0: c0 + bl])
                 table = self._kv.table[idx + row0]
             buf.pos0.fill_(c0)
@@ -336,7 +336,10 @@ class HipEngine:
             last = [(i, r) for i, r in enumerate(active) if c0 <= lps[r] - 1 < c0 + bl]
             if last:
                 hid = buf.hidden.view(na, bl, D)
-                sos[[r for _, r in last], 0] = hid[[i for i, _ in last], [lps[r] - 1 - c0 for _, r in last]]
+                dst = to_device_async([r for _, r in last], torch.long, dev)
+                src_row = to_device_async([i for i, _ in last], torch.long, dev)
+                src_pos = to_device_async([lps[r] - 1 - c0 for _, r in last], torch.long, dev)
+                sos[dst, 0] = hid[src_row, src_pos]
         return sos
 
     def causal_forward(self, emb: Tensor) -> Tensor:

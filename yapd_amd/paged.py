@@ -22,6 +22,16 @@ PAGE_SIZE = 16
 HEAD_DIM = 64
 
 
+def to_device_async(data, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """Host data (list or array) on ``device`` without a host synchronisation: staged through
+    pinned memory and copied on the current stream (a copy from pageable memory would wait for
+    every kernel already queued)."""
+    t = torch.as_tensor(np.asarray(data), dtype=dtype)
+    if torch.device(device).type != "cuda":
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 class PagedKV:
     """Per-layer page pools plus a host-side page allocator and device page table."""
 
@@ -63,8 +73,8 @@ class PagedKV:
     def copy_row_pages(self, src_row: int, dst_row: int, n_positions: int) -> None:
         """Copy the pages holding positions ``[0, n_positions)`` of one row to another, every layer."""
         npg = (n_positions + PAGE_SIZE - 1) // PAGE_SIZE
-        src = torch.from_numpy(self.table_host[src_row, :npg].astype(np.int64)).to(self.device)
-        dst = torch.from_numpy(self.table_host[dst_row, :npg].astype(np.int64)).to(self.device)
+        src = to_device_async(self.table_host[src_row, :npg], torch.int64, self.device)
+        dst = to_device_async(self.table_host[dst_row, :npg], torch.int64, self.device)
         for pool in self.pools:
             pool.index_copy_(0, dst, pool.index_select(0, src))
 
@@ -76,10 +86,10 @@ class AttnPlan:
                  target_items: int = 192, min_split_keys: int = 1024):
         work, merge, n_slots = kernels.attn_plan(kv_len, target_items=target_items, min_split_keys=min_split_keys)
         self.kv_len_host = [int(x) for x in kv_len]
-        self.work = torch.from_numpy(work).to(device)
-        self.merge = torch.from_numpy(merge).to(device) if merge.shape[0] else None
+        self.work = to_device_async(work, torch.int32, device)
+        self.merge = to_device_async(merge, torch.int32, device) if merge.shape[0] else None
         self.n_slots = n_slots
-        self.kv_len = torch.tensor(self.kv_len_host, dtype=torch.int32, device=device)
+        self.kv_len = to_device_async(self.kv_len_host, torch.int32, device)
         if n_slots:
             self.part_o = torch.empty(n_slots, bl, n_heads, HEAD_DIM, dtype=torch.float32, device=device)
             self.part_ml = torch.empty(n_slots, bl, n_heads, 2, dtype=torch.float32, device=device)

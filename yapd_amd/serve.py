@@ -36,7 +36,7 @@ import torch
 from . import kernels
 from .embed import SpeechEmbedder
 from .engines.hip import HipEngine
-from .paged import PAGE_SIZE
+from .paged import PAGE_SIZE, to_device_async
 from .scoring import BlockScorer
 from .voc_stream import maybe_vocode
 
@@ -368,15 +368,16 @@ class HipFlashEngine:
         sos = self.eng.prefix_forward_rows(base * nb, embs)
         G = len(take)
         self.shift_ctx[base * nb:(base + G) * nb] = sos
+        # the new slots are base..base+G-1: one fill or one upload per state tensor
+        sl = slice(base, base + G)
+        self.blk_start[sl] = 0
+        self.k_step[sl] = 0
+        self.is_commit[sl] = 0
+        self.xt[sl] = self.MASK
+        lps = [int(q.prefix.shape[0]) for q in take]
+        self.cache_len[sl] = to_device_async(lps, self.cache_len.dtype, self.dev)
+        self.n_speech[sl] = to_device_async([q.n_speech for q in take], self.n_speech.dtype, self.dev)
         now = time.perf_counter()
         for g, q in enumerate(take):
-            s = base + g
-            lp = int(q.prefix.shape[0])
-            self.blk_start[s] = 0
-            self.k_step[s] = 0
-            self.is_commit[s] = 0
-            self.cache_len[s] = lp
-            self.n_speech[s] = q.n_speech
-            self.xt[s] = self.MASK
-            q.slot, q.lp, q.cpu_len, q.known_tick, q.t_admit = s, lp, lp, self.tick_id, now
+            q.slot, q.lp, q.cpu_len, q.known_tick, q.t_admit = base + g, lps[g], lps[g], self.tick_id, now
             self.active.append(q)
