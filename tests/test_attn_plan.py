@@ -46,3 +46,21 @@ def test_plan_rejects_bad_lengths():
         kernels.attn_plan([10, 0, 5])
     with pytest.raises(ValueError):
         kernels.attn_plan([10], min_split_keys=16)
+
+
+def test_host_uploads_keep_values_dtype_and_shape():
+    """``to_device_async`` (plan, row-list and index uploads) converts lists, numpy arrays and
+    numpy slices exactly; on the CPU it is a plain conversion (the pinned, stream-ordered copy is
+    the GPU branch, exercised by every engine test)."""
+    import numpy as np
+    import torch
+    from yapd_amd.paged import AttnPlan, to_device_async
+    assert torch.equal(to_device_async([3, 1, 2], torch.long, torch.device("cpu")), torch.tensor([3, 1, 2]))
+    arr = np.arange(12, dtype=np.int32).reshape(3, 4)
+    t = to_device_async(arr, torch.int32, "cpu")
+    assert t.dtype == torch.int32 and torch.equal(t, torch.from_numpy(arr))
+    t = to_device_async(arr[1, :3], torch.int64, "cpu")
+    assert t.dtype == torch.int64 and t.tolist() == [4, 5, 6]
+    plan = AttnPlan([700, 40, 1600], 16, 16, torch.device("cpu"))
+    assert plan.work.dtype == torch.int32 and plan.work.shape[1] == 4
+    assert plan.kv_len.tolist() == [700, 40, 1600]
