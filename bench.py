@@ -26,8 +26,8 @@ times the oracle (torch on the host cores) on a bounded sample of the same
 step.
 
 ``secondary`` (skipped with ``--no-secondary``) carries, from the same run,
-the headline figures of the prefill, serve and attention-stress workloads
-below (about 15 s more).
+the headline figures of the prefill, serve, attention-stress and vocoder
+workloads below (about 15 s more).
 
 ``--workload serve`` runs the continuous-batching engine (server defaults:
 128 slots, block 16, K = 10, temperature 0.6, position temperature 5, CFG 1)
@@ -51,6 +51,7 @@ back to back over 256 sequences with log-uniform [64, 2048] prefixes, block
 from __future__ import annotations
 
 import argparse
+import copy
 import json
 import math
 import os
@@ -156,7 +157,9 @@ def main():
         print(json.dumps(serve(args, dev)), flush=True)
         return
     if args.workload == "vocoder":
-        vocoder_workload(args, dev)
+        out = vocoder_workload(args, dev)
+        if out is not None:
+            print(json.dumps(out), flush=True)
         return
     if args.workload == "prefill":
         prefill_workload(args, dev)
@@ -318,8 +321,9 @@ def main():
 def secondary_workloads(args, dev, model, eng, prefixes, lps):
     """The other workloads' headline figures, measured in the same run after the step: the prefix
     prefill of the step's 512 rows (through the step's engine, rewriting the same KV), continuous
-    batching on the same model, and 30 layers of attention over the stress shape.  The full
-    objects come from ``--workload prefill | serve | attn_stress``."""
+    batching on the same model, 30 layers of attention over the stress shape, and the vocoder's
+    elementwise family and chunk stitch.  The full objects come from ``--workload prefill | serve |
+    attn_stress | vocoder``."""
     L, D = args.layers, 1024
     embs = [p.to(dev) for p in prefixes + prefixes]
     ms_pf, wall_pf = time_prefill(eng, embs, 2, dev)
@@ -331,6 +335,10 @@ def secondary_workloads(args, dev, model, eng, prefixes, lps):
     torch.cuda.empty_cache()
     st = attn_stress(args, dev)
     torch.cuda.empty_cache()
+    voc_args = copy.copy(args)
+    voc_args.no_cpu_baseline = True
+    vc = vocoder_workload(voc_args, dev)
+    torch.cuda.empty_cache()
     return {
         "prefill": {"value": round(tokens / (ms_pf * 1e-3), 1), "unit": "prefix tokens/s", "ms": round(ms_pf, 3),
                     "wall_ms": round(wall_pf, 2), "prefix_tokens": tokens, "rows": len(lps), "layers": L,
@@ -341,6 +349,10 @@ def secondary_workloads(args, dev, model, eng, prefixes, lps):
         "attn_stress": {"value": st["value"], "unit": st["unit"], "ms_30_layers": st["ms_per_step"],
                         "frac": st["roofline"]["frac"], "sequences": st["config"]["sequences"],
                         "block": st["config"]["block"], "layers": st["config"]["layers"]},
+        "vocoder": {"value": vc["value"], "unit": vc["unit"], "kernel": "residual_bias_snake",
+                    "frac": vc["roofline"]["frac"], "shape": [vc["config"]["batch"], vc["config"]["channels"],
+                                                              vc["config"]["samples"]],
+                    "stitch_us": vc["kernels"]["stitch"]["us"], "stitch_jobs": vc["kernels"]["stitch"]["jobs"]},
     }
 
 
@@ -516,7 +528,7 @@ def vocoder_workload(args, dev):
         torch.cuda.synchronize(dev)
         print(json.dumps({"kernel_sample": "residual_bias_snake [%d, %d, %d] x3; copy %d bytes x3"
                                            % (B, C, T, COPY_BYTES)}))
-        return
+        return None
     it = [0]
 
     def pick():
@@ -556,14 +568,14 @@ def vocoder_workload(args, dev):
         cpu = {"value": round(passes * 4 * 4 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": f"residual_bias_snake on [{B}, {C}, {T}] x {passes} with the numpy oracle (float64 Snake), "
                          f"one thread, {dt:.1f} s"}
-    print(json.dumps({
+    return {
         "metric": "HiFT vocoder elementwise HBM GB/s (residual_bias_snake)", "value": dom["gbs"], "unit": "GB/s",
         "n_gpus": 1, "ms_per_step": round(dom["us"] / 1e3, 4), "higher_is_better": True, "dtype": "f32",
         "data": "synthetic (N(0,1) activations, alpha U[0.2, 2.2], bias N(0, 0.01))",
         "config": {"workload": "HiFT last-stage elementwise ops", "batch": B, "channels": C, "samples": T},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "bytes_per_launch": 4 * 4 * n, "traffic": traffic},
-        "kernels": res, "cpu_baseline": cpu}), flush=True)
+        "kernels": res, "cpu_baseline": cpu}
 
 
 def stitch_sample(args, dev, g):
