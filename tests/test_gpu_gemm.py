@@ -23,10 +23,13 @@ def rel_err(out, ref):
     return ((out.float() - ref.float()).abs().max() / ref.float().abs().max().clamp_min(1e-6)).item()
 
 
-# The last three take the large-tile (256 x 256) path: >= 256 output tiles,
-# M not a multiple of 256 in two of them.
+# (16384 // 8, 8192, 1024), (2000, 8192, 1024), (4100, 4096, 2048) take the large-tile (256 x 256)
+# path: >= 256 output tiles, M not a multiple of 256 in two of them.  M = 3072, N = 1024 is a grid of
+# one 128 x 128 tile per CU, which runs three LDS stages: K = 64 / 128 / 192 give one, two and three
+# k-tiles (the stage hand-off's short and tail cases); (3000, 1000, 4096) a ragged grid of that kind.
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 3072, 1024), (1024, 1024, 4096), (37, 8194, 1024),
-                                   (16384 // 8, 8192, 1024), (2000, 8192, 1024), (4100, 4096, 2048)])
+                                   (16384 // 8, 8192, 1024), (2000, 8192, 1024), (4100, 4096, 2048),
+                                   (3072, 1024, 64), (3072, 1024, 128), (3072, 1024, 192), (3000, 1000, 4096)])
 def test_gemm_bf16(dev, M, N, K):
     A = rnd(M, K, seed=1)
     W = rnd(N, K, std=0.02, seed=2)
