@@ -12,8 +12,10 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-# (16384, 1000, 1024): the large-M kernel with a partial last column tile
-@pytest.mark.parametrize("M,N,K", [(256, 3072, 1024), (8192, 1024, 4096), (37, 200, 128), (16384, 1000, 1024)])
+# (16384, 1000, 1024): the large-M kernel with a partial last column tile; (1024, 1000, 64) and
+# (512, 200, 128): the direct-load 128 x 128 kernel with one and two k-tiles and partial tiles
+@pytest.mark.parametrize("M,N,K", [(256, 3072, 1024), (8192, 1024, 4096), (37, 200, 128), (16384, 1000, 1024),
+                                   (1024, 1000, 64), (512, 200, 128)])
 def test_qgemm_vs_fp32_dequant(dev, bits, M, N, K):
     g = torch.Generator().manual_seed(M + N + bits)
     w = torch.randn(N, K, generator=g) * 0.02
