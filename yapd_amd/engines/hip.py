@@ -29,7 +29,7 @@ import torch
 from torch import Tensor
 
 from .. import kernels
-from ..paged import PAGE_SIZE, AttnPlan, PagedKV, to_device_async
+from ..paged import PAGE_SIZE, AttnPlan, PagedKV, copy_from_host_async, to_device_async
 
 logger = logging.getLogger(__name__)
 
@@ -372,7 +372,7 @@ class HipEngine:
         self._check_capacity(starts, bl)
         buf = self._buffers(B, bl)
         buf.emb.copy_(block_emb.reshape(B * bl, D))
-        buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+        copy_from_host_async(buf.pos0, starts)
         plan = self._plan([s + bl for s in starts], bl)
         self._run(buf, plan, plan.kv_len)
         return buf.hidden.view(B, bl, D).clone()
@@ -400,7 +400,7 @@ class HipEngine:
             m.final_eps = self._w[li + 1]["eps_in"]
         buf = self._buffers(B, bl)
         buf.emb.copy_(x.reshape(B * bl, D))
-        buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+        copy_from_host_async(buf.pos0, starts)
         plan = self._plan([s + bl for s in starts], bl)
         ws = self._workspace(buf, plan)
         kernels.check(kernels.load_library().yapd_t3_block_forward(
@@ -464,7 +464,7 @@ class HipEngine:
         bl = self._g_bl
         self._check_capacity(starts, bl)
         buf = self._buffers(self._batch_size, bl)
-        buf.pos0.copy_(torch.tensor(starts, dtype=torch.int32))
+        copy_from_host_async(buf.pos0, starts)
         self._g_plan.update([s + bl for s in starts])
         self._g_cs_key = key
 
@@ -503,9 +503,10 @@ class _GraphPlan:
         work, merge, n_slots = kernels.attn_plan(kv_len, target_items=self.target)
         if work.shape[0] > self.work.shape[0] or n_slots > self.n_slots:
             raise RuntimeError("attention plan exceeds the captured capacity")
-        self.work[: work.shape[0]].copy_(torch.from_numpy(work))
+        # stream-ordered uploads from pinned staging: no host sync between blocks
+        copy_from_host_async(self.work[: work.shape[0]], work)
         if merge.shape[0]:
-            self.merge[: merge.shape[0]].copy_(torch.from_numpy(merge))
-        self.counts.copy_(torch.tensor([work.shape[0], merge.shape[0]], dtype=torch.int32))
+            copy_from_host_async(self.merge[: merge.shape[0]], merge)
+        copy_from_host_async(self.counts, [work.shape[0], merge.shape[0]])
         self.n_merge_live = int(merge.shape[0])  # rows split by the current plan (host copy)
-        self.kv_len.copy_(torch.tensor(kv_len, dtype=torch.int32))
+        copy_from_host_async(self.kv_len, kv_len)

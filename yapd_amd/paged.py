@@ -32,6 +32,17 @@ def to_device_async(data, dtype: torch.dtype, device: torch.device) -> torch.Ten
     return t.pin_memory().to(device, non_blocking=True)
 
 
+def copy_from_host_async(dst: torch.Tensor, data) -> None:
+    """``dst.copy_(data)`` for host data (list or array) without a host synchronisation: staged
+    through pinned memory and copied on the current stream.  Not for use inside a graph capture
+    (the copy would keep reading a recycled staging buffer on every replay)."""
+    t = torch.as_tensor(np.asarray(data)).to(dst.dtype)
+    if dst.device.type != "cuda":
+        dst.copy_(t)
+        return
+    dst.copy_(t.pin_memory(), non_blocking=True)
+
+
 class PagedKV:
     """Per-layer page pools plus a host-side page allocator and device page table."""
 
