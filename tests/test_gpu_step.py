@@ -42,17 +42,17 @@ ROWS = 2 * PAIRS
 SAMPLE = (0, 77, 255)  # pairs whose cond and null rows go through the CPU oracle
 
 
-def block_tokens(seed):
+def block_tokens(seed, pairs=PAIRS, bl=BL):
     """Per pair a step index k ~ U{0..7} and a block whose masked count follows the
     OmniVoice schedule after k steps; a few unmasked positions hold STOP."""
     g = torch.Generator().manual_seed(seed)
-    k_step = torch.randint(0, 8, (PAIRS,), generator=g)
-    sched = omnivoice_unmask_schedule(BL, K, T_SHIFT)
-    xt = torch.randint(0, CODEC_V, (PAIRS, BL), generator=g)
-    for p in range(PAIRS):
-        n_masked = BL - sum(sched[: int(k_step[p])])
-        xt[p, torch.randperm(BL, generator=g)[:n_masked]] = MASK_ID
-    stop_rows = torch.randint(0, PAIRS, (8,), generator=g)
+    k_step = torch.randint(0, 8, (pairs,), generator=g)
+    sched = omnivoice_unmask_schedule(bl, K, T_SHIFT)
+    xt = torch.randint(0, CODEC_V, (pairs, bl), generator=g)
+    for p in range(pairs):
+        n_masked = bl - sum(sched[: int(k_step[p])])
+        xt[p, torch.randperm(bl, generator=g)[:n_masked]] = MASK_ID
+    stop_rows = torch.randint(0, pairs, (8,), generator=g)
     for p in stop_rows.tolist():
         free = (xt[p] != MASK_ID).nonzero().flatten()
         if len(free):
@@ -90,13 +90,14 @@ def embedded_reference(model, xt):
 def eager_step(w, starts):
     """block_forward + gemm_head_shift + a separate BlockScorer on the step's inputs."""
     eng, model, step = w["eng"], w["model"], w["step"]
+    pairs, bl = w.get("pairs", PAIRS), w.get("bl", BL)
     emb = embedded_reference(model, torch.cat([step.xt, step.xt], 0))
     hid = eng.block_forward(emb, starts)
     V = model.speech_head.weight.shape[0]
-    logits_buf = torch.zeros(ROWS, BL, (V + 7) // 8 * 8, dtype=torch.bfloat16, device=hid.device)
+    logits_buf = torch.zeros(2 * pairs, bl, (V + 7) // 8 * 8, dtype=torch.bfloat16, device=hid.device)
     logits = logits_buf[..., :V]
     kernels.gemm_head_shift(hid, eng._g_shift_ctx, eng._head_w, logits)
-    scorer = BlockScorer(n_pairs=PAIRS, block_size=BL, log_prior=w["log_prior"].to(hid.device), mask_id=MASK_ID,
+    scorer = BlockScorer(n_pairs=pairs, block_size=bl, log_prior=w["log_prior"].to(hid.device), mask_id=MASK_ID,
                          stop_id=STOP_ID, num_steps=K, time_shift_tau=TAU, omnivoice_t_shift=T_SHIFT, cfg_scale=W,
                          device=hid.device)
     res = scorer(logits, step.xt, step.k_step, layout="stacked")
@@ -105,9 +106,10 @@ def eager_step(w, starts):
 
 
 def decisions_vs_oracle(res, logits, w):
+    pairs, bl = w.get("pairs", PAIRS), w.get("bl", BL)
     lf = logits.float().cpu()
-    lc, lu = lf[:PAIRS].contiguous(), lf[PAIRS:].contiguous()
-    sched = torch.tensor(omnivoice_unmask_schedule(BL, K, T_SHIFT))
+    lc, lu = lf[:pairs].contiguous(), lf[pairs:].contiguous()
+    sched = torch.tensor(omnivoice_unmask_schedule(bl, K, T_SHIFT))
     q = torch.tensor(quantile_fractions(TAU, K), dtype=torch.float32)
     xt, ks = w["step"].xt.cpu(), w["step"].k_step.cpu()
 
@@ -119,7 +121,7 @@ def decisions_vs_oracle(res, logits, w):
     torch.testing.assert_close(res.pmi.cpu(), ref["pmi"], rtol=2e-5, atol=2e-5)
     ref, n_near = settle_confidence_near_ties(res, ref, ks, sched, q, K=K, tau=TAU, mask_id=MASK_ID,
                                               stop_id=STOP_ID)
-    print(f"decisions: {n_near} of {PAIRS} pairs settled at confidence near-ties")
+    print(f"decisions: {n_near} of {pairs} pairs settled at confidence near-ties")
     assert torch.equal(res.unmask.cpu().bool(), ref["do_unmask"])
     assert torch.equal(res.xt.cpu(), ref["xt_new"])
     assert torch.equal(res.n_mask_after.cpu().long(), ref["n_mask_after"])
