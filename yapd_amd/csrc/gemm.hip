@@ -1003,54 +1003,81 @@ struct NormParams {
   uint16_t* out;
 };
 
-// One wave per row; D = 1024 -> 16 bf16 per lane (two 16-byte chunks).
+// Two rows per wave; D = 1024 -> 16 bf16 per lane and row (two 16-byte chunks).  All of a
+// wave's loads (both rows and the gain) are requested before the first reduction: one row per
+// wave with the gain read after the reduction took 12.1 us at 16384 x 1024 against 11.3 us
+// (four rows per wave: 12.35 us), bit-identical.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const NormParams p) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int kRows = 2;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRows;
   const int lane = threadIdx.x & 63;
-  if (row >= p.M) return;
-  const int64_t base = static_cast<int64_t>(row) * p.D;
+  if (row0 >= p.M) return;
   constexpr int kMaxChunks = 4;  // D <= 2048
-  u32x4_t xv[kMaxChunks];
   const int nch = p.D / (64 * 8);
-  float ss = 0.f;
+  u32x4_t wv[kMaxChunks];
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    if (c >= nch) break;
-    const int64_t off = base + (c * 64 + lane) * 8;
-    u32x4_t x;
-    if (p.delta) {
-      const u32x4_t r = ldg16(p.residual + off);
-      const u32x4_t dl = ldg16(p.delta + off);
+  for (int c = 0; c < kMaxChunks; ++c)
+    if (c < nch) wv[c] = ldg16(p.w + (c * 64 + lane) * 8);
+  u32x4_t xv[kRows][kMaxChunks];
+  float ss[kRows];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) x[w] = pack_bf16x2(bf16lo(r[w]) + bf16lo(dl[w]), bf16hi(r[w]) + bf16hi(dl[w]));
-      *reinterpret_cast<u32x4_t*>(p.residual + off) = x;
-    } else {
-      x = ldg16(p.x + off);
-      if (p.residual) *reinterpret_cast<u32x4_t*>(p.residual + off) = x;  // residual = clone(x)
-    }
-    xv[c] = x;
+  for (int rr = 0; rr < kRows; ++rr) {
+    ss[rr] = 0.f;
+    const int row = min(row0 + rr, p.M - 1);
+    const int64_t base = static_cast<int64_t>(row) * p.D;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float a = bf16lo(x[w]), b = bf16hi(x[w]);
-      ss += a * a + b * b;
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c >= nch) break;
+      const int64_t off = base + (c * 64 + lane) * 8;
+      u32x4_t x;
+      if (p.delta) {
+        const u32x4_t r = ldg16(p.residual + off);
+        const u32x4_t dl = ldg16(p.delta + off);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) x[w] = pack_bf16x2(bf16lo(r[w]) + bf16lo(dl[w]), bf16hi(r[w]) + bf16hi(dl[w]));
+        if (row0 + rr < p.M) *reinterpret_cast<u32x4_t*>(p.residual + off) = x;
+      } else {
+        x = ldg16(p.x + off);
+        if (p.residual && row0 + rr < p.M) *reinterpret_cast<u32x4_t*>(p.residual + off) = x;
+      }
+      xv[rr][c] = x;
     }
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float rs = rsqrtf(ss / static_cast<float>(p.D) + p.eps);
+  for (int rr = 0; rr < kRows; ++rr) {
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    if (c >= nch) break;
-    const int64_t off = base + (c * 64 + lane) * 8;
-    const u32x4_t wv = ldg16(p.w + (c * 64 + lane) * 8);
-    u32x4_t y;
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c >= nch) break;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float a = bf16lo(wv[w]) * round_bf16(bf16lo(xv[c][w]) * rs);
-      const float b = bf16hi(wv[w]) * round_bf16(bf16hi(xv[c][w]) * rs);
-      y[w] = pack_bf16x2(a, b);
+      for (int w = 0; w < 4; ++w) {
+        const float a = bf16lo(xv[rr][c][w]), b = bf16hi(xv[rr][c][w]);
+        ss[rr] += a * a + b * b;
+      }
     }
-    *reinterpret_cast<u32x4_t*>(p.out + off) = y;
+  }
+#pragma unroll
+  for (int rr = 0; rr < kRows; ++rr) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss[rr] += __shfl_xor(ss[rr], o, 64);
+  }
+#pragma unroll
+  for (int rr = 0; rr < kRows; ++rr) {
+    if (row0 + rr >= p.M) break;
+    const float rs = rsqrtf(ss[rr] / static_cast<float>(p.D) + p.eps);
+    const int64_t base = static_cast<int64_t>(row0 + rr) * p.D;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c >= nch) break;
+      const int64_t off = base + (c * 64 + lane) * 8;
+      u32x4_t y;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a = bf16lo(wv[c][w]) * round_bf16(bf16lo(xv[rr][c][w]) * rs);
+        const float b = bf16hi(wv[c][w]) * round_bf16(bf16hi(xv[rr][c][w]) * rs);
+        y[w] = pack_bf16x2(a, b);
+      }
+      *reinterpret_cast<u32x4_t*>(p.out + off) = y;
+    }
   }
 }
 
@@ -1332,7 +1359,7 @@ int rmsnorm_launch(const void* delta, void* residual, const void* x, const void*
                    void* out, hipStream_t st) {
   NormParams p{static_cast<const uint16_t*>(delta), static_cast<uint16_t*>(residual), static_cast<const uint16_t*>(x),
                static_cast<const uint16_t*>(w), eps, M, D, static_cast<uint16_t*>(out)};
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((M + 3) / 4), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((M + 7) / 8), dim3(256), 0, st, p);
   YAPD_LAUNCH_CHECK("rmsnorm_kernel launch");
   return YAPD_OK;
 }
