@@ -255,6 +255,28 @@ def test_rows_do_not_depend_on_batch_size(dev, epi):
         assert torch.equal(res[0][1][pages].cpu(), pool[pages].cpu()), M
 
 
+def test_down_rows_do_not_depend_on_batch_size_or_tile_order(dev):
+    """down_proj + residual (N = 1024, K = 4096) at the sizes whose grids take
+    each tile order: M = 32768 and 24576 are multi-round grids of 256 x 256
+    tiles in the columns-fastest XCD band order, M = 16384 a single round in the
+    band order, M = 4096 the 128 x 128 kernel.  Every row of each smaller call
+    equals the largest call's bit for bit."""
+    N, K = 1024, 4096
+    sizes = (32768, 24576, 16384, 4096)
+    A = rnd(sizes[0], K, std=0.05, seed=51).to(dev)
+    W = rnd(N, K, std=0.02, seed=52).to(dev)
+    R = rnd(sizes[0], N, seed=53).to(dev)
+    outs = []
+    for M in sizes:
+        C = R[:M].clone()
+        kernels.gemm_bf16_residual(A[:M], W, C)
+        outs.append(C.cpu())
+    for M, out in zip(sizes[1:], outs[1:]):
+        assert torch.equal(outs[0][:M], out), M
+    ref = R[:256].cpu().float() + (A[:256].cpu().float() @ W.cpu().float().T).bfloat16().float()
+    assert rel_err(outs[0][:256], ref) <= 8e-3
+
+
 def test_narrow_last_column_tile_is_split_bit_identically(dev):
     """N = 32 x 256 + 2 (the speech head): when the 2-column tile would add a
     round of 256 x 256 tiles, those columns run as a second launch on 64 x 64

@@ -84,7 +84,7 @@ struct GemmParams {
   int64_t ldq;  // uint32 words per row
   const uint16_t* qscale;
   const uint16_t* qbias;
-  int xcd_band;  // 1: XCD-banded tile order (set by the launcher)
+  int xcd_band;  // 1, 2: XCD-banded tile orders (set by the launcher)
 };
 
 __device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
@@ -395,14 +395,20 @@ __device__ __forceinline__ uint32_t dq_pair(uint32_t word, int shift, float sc, 
 // tiles of one A row block land on different XCDs, so every one of them
 // fetches that block; with `band` set, XCD j instead takes the band of row
 // tiles [j R/8, (j+1) R/8) across all column tiles, and each A row block is
-// fetched into one L2.  (For multi-round grids the row-major order measured
-// faster and is kept.)
+// fetched into one L2.  Mode 2 is for multi-round grids with few column tiles
+// and large A row blocks (down at M > 16384): the same bands, columns
+// fastest, so the workgroups an XCD runs at once cover whole row blocks (8 row
+// blocks x 4 columns for N = 1024) and each A row block is fetched once, by
+// one XCD, while in row-major order 4 XCDs fetch it.  (Multi-round grids with
+// many column tiles, gate/up and QKV, keep the row-major order: the banded
+// one measured slower there.)
 __device__ __forceinline__ int2 tile_coords(int xcd_band) {
   const int C = gridDim.x, R = gridDim.y;
   const int L = blockIdx.x + C * blockIdx.y;
   if (!xcd_band || R % 8 != 0) return make_int2(blockIdx.x, blockIdx.y);
   const int band = R / 8;
   const int j = L % 8, i = L / 8;
+  if (xcd_band == 2) return make_int2(i % C, j * band + i / C);
   return make_int2(i / band, j * band + i % band);  // (column tile, row tile)
 }
 
@@ -1159,7 +1165,11 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   // once they give one workgroup per CU.
   const int64_t big_tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
   if (big_tiles >= (BQ == 0 ? cu_count() * 3 / 4 : cu_count())) {
-    p.xcd_band = big_tiles <= cu_count() ? 1 : 0;
+    // banded orders: single-round grids; multi-round grids with few column
+    // tiles and a long K (down at M > 16384: 336 -> 276 us at M = 32768,
+    // 263 -> 244 us at M = 24576; o with K = 1024 measured 90 -> 96 us at
+    // M = 32768 and keeps the row-major order)
+    p.xcd_band = big_tiles <= cu_count() ? 1 : (p.N + 255) / 256 <= 8 && p.K >= 2048 ? 2 : 0;
     if constexpr (BQ == 0) {
       if constexpr (EPI == kEpiStore) {
         // A last column tile of at most 64 columns that would add a round of
