@@ -396,12 +396,13 @@ __device__ __forceinline__ uint32_t dq_pair(uint32_t word, int shift, float sc, 
 // fetches that block; with `band` set, XCD j instead takes the band of row
 // tiles [j R/8, (j+1) R/8) across all column tiles, and each A row block is
 // fetched into one L2.  Mode 2 is for multi-round grids with few column tiles
-// and large A row blocks (down at M > 16384): the same bands, columns
-// fastest, so the workgroups an XCD runs at once cover whole row blocks (8 row
-// blocks x 4 columns for N = 1024) and each A row block is fetched once, by
-// one XCD, while in row-major order 4 XCDs fetch it.  (Multi-round grids with
-// many column tiles, gate/up and QKV, keep the row-major order: the banded
-// one measured slower there.)
+// and large A row blocks (down at M > 16384) and for QKV: the same bands,
+// columns fastest, so the workgroups an XCD runs at once cover whole row
+// blocks (8 row blocks x 4 columns for N = 1024) and each A row block is
+// fetched once, by one XCD, while in row-major order 4 XCDs fetch it.
+// (gate/up, 32 column tiles, keeps the row-major order, in which each XCD
+// keeps the same 4 column tiles of W in its L2 for every round; the banded
+// order measured slower there.)
 __device__ __forceinline__ int2 tile_coords(int xcd_band) {
   const int C = gridDim.x, R = gridDim.y;
   const int L = blockIdx.x + C * blockIdx.y;
@@ -1168,8 +1169,11 @@ int launch_gemm(GemmParams p, hipStream_t st) {
     // banded orders: single-round grids; multi-round grids with few column
     // tiles and a long K (down at M > 16384: 336 -> 276 us at M = 32768,
     // 263 -> 244 us at M = 24576; o with K = 1024 measured 90 -> 96 us at
-    // M = 32768 and keeps the row-major order)
-    p.xcd_band = big_tiles <= cu_count() ? 1 : (p.N + 255) / 256 <= 8 && p.K >= 2048 ? 2 : 0;
+    // M = 32768 and keeps the row-major order), and QKV's 12 column tiles
+    // (step 22.71 -> 22.64 ms in three alternating pairs on one box; the
+    // rows-fastest band order measured 23.17 ms there)
+    const bool band2 = ((p.N + 255) / 256 <= 8 && p.K >= 2048) || EPI == kEpiQkv;
+    p.xcd_band = big_tiles <= cu_count() ? 1 : band2 ? 2 : 0;
     if constexpr (BQ == 0) {
       if constexpr (EPI == kEpiStore) {
         // A last column tile of at most 64 columns that would add a round of
