@@ -260,6 +260,22 @@ int yapd_t3_block_forward(const yapd_t3_model* model, const yapd_t3_workspace* w
                           void* hidden_out, const void* head_w, int vocab, const void* shift_ctx, void* logits,
                           int64_t ld_logits, void* stream);
 
+/* One causal chunk of a prefix prefill (engines/flashinfer.py:prefix_forward
+ * :678-854, the chunked causal forward that writes each row's prefix KV)
+ * over packed rows: no row is padded to the chunk length.  Row r's tokens
+ * are rows [row_start[r], row_start[r+1]) of tok_emb [n_tokens, D] (at most
+ * max_q <= 64 per row), at positions pos0[r], pos0[r] + 1, ...; tok_row
+ * [n_tokens] names each token's row; kv_len[r] = pos0[r] + the row's token
+ * count (row_start, tok_row, pos0, kv_len: device int32).  The workspace's
+ * activations hold n_tokens rows, its attention plan is yapd_attn_plan over
+ * kv_len with bl = max_q, and its partials are [n_slots, max_q, H, ...].
+ * hidden_out [n_tokens, D] receives the final-normed hidden.  The row map's
+ * indices are clamped on the device (a bad map cannot fault); the layer and
+ * workspace rules of yapd_t3_block_forward are checked before any launch. */
+int yapd_t3_prefill_packed(const yapd_t3_model* model, const yapd_t3_workspace* ws, const void* tok_emb,
+                           int n_tokens, int rows, int max_q, const int32_t* row_start, const int32_t* tok_row,
+                           const int32_t* pos0, const int32_t* kv_len, void* hidden_out, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * Continuous-batching tick bookkeeping (server/engine.py:522-612, the state
  * updates of FlashEngine._step_gpu after the scorer).  For slots s <

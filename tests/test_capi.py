@@ -170,6 +170,22 @@ def test_block_forward_checks_every_layer_rule_before_launching(override, msg):
     assert rc == EINVAL and msg in lib.yapd_last_error(), lib.yapd_last_error()
 
 
+@pytest.mark.parametrize("n_tokens,rows,max_q,msg", [
+    (0, 4, 64, b"n_tokens"), (300, 4, 64, b"n_tokens <= rows * max_q"), (10, 4, 65, b"max_q <= 64"),
+    (10, 0, 64, b"rows >= 1")])
+def test_packed_prefill_checks_before_launching(n_tokens, rows, max_q, msg):
+    lib = kernels.load_library()
+    model, ws, _keep = _block_forward_args()
+    rc = lib.yapd_t3_prefill_packed(ctypes.byref(model), ctypes.byref(ws), P, n_tokens, rows, max_q, P, P, P, P, P,
+                                    None)
+    assert rc == EINVAL and msg in lib.yapd_last_error(), lib.yapd_last_error()
+    model, ws, _keep = _block_forward_args(n_heads=6)
+    rc = lib.yapd_t3_prefill_packed(ctypes.byref(model), ctypes.byref(ws), P, 10, 4, 64, P, P, P, P, P, None)
+    assert rc == EINVAL and b"n_heads must be a multiple of 4" in lib.yapd_last_error()
+    rc = lib.yapd_t3_prefill_packed(ctypes.byref(model), ctypes.byref(ws), P, 10, 4, 64, None, P, P, P, P, None)
+    assert rc == EINVAL and b"NULL pointer" in lib.yapd_last_error()
+
+
 def test_block_forward_rejects_incomplete_layer_and_head():
     lib = kernels.load_library()
     model, ws, layers = _block_forward_args()

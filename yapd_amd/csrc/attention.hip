@@ -53,9 +53,20 @@ struct AttnParams {
   float* part_ml;       // [slots, bl, H, 2]
   int n_slots;          // partials exist for slots [0, n_slots); an item naming another slot writes nothing
   float scale_log2;     // softmax scale * log2(e)
-  int causal;           // 1: query i of the block sees keys < kv_len - bl + i + 1 (prefix prefill)
+  int causal;           // 1: query i of the block sees keys < kv_len - n_q(row) + i + 1 (prefix prefill)
   uint16_t* out;        // [rows, bl, H, 64]
+  // Packed queries (NULL: row r's bl queries are rows r*bl ..): row r's queries
+  // are q / out rows [q_start[r], q_start[r+1]) of n_q, at most bl of them.
+  const int32_t* q_start;
+  int n_q;
 };
+
+// First query row of row r in q / out and its query count.
+__device__ __forceinline__ int2 row_queries(const int32_t* q_start, int n_q, int r, int bl) {
+  if (q_start == nullptr) return make_int2(r * bl, bl);
+  const int qs = min(max(q_start[r], 0), n_q);
+  return make_int2(qs, min(max(q_start[r + 1] - qs, 0), min(bl, n_q - qs)));
+}
 
 __device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
@@ -115,6 +126,8 @@ attn_paged_kernel(const AttnParams P) {
   const int g = lane >> 4;   // lane group: key group / head-dim group
   const int n = lane & 15;   // query within a 16-query tile / row within an M tile
   const int H = P.H, bl = P.bl;
+  const int2 rq = row_queries(P.q_start, P.n_q, r, bl);
+  const int qs = rq.x, qc = rq.y;  // the row's first query row and query count
 
   // Q^T fragments (B operand): lane holds Q[q = qt*16 + n][hd = ks*32 + 8g .. +7].
   bf16x8_t qf[NQT][2];
@@ -124,7 +137,7 @@ attn_paged_kernel(const AttnParams P) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       u32x4_t v = {0u, 0u, 0u, 0u};
-      if (q < bl) v = load16(P.q + ((static_cast<int64_t>(r) * bl + q) * H + h) * kHeadDim + ks * 32 + 8 * g);
+      if (q < qc) v = load16(P.q + ((static_cast<int64_t>(qs) + q) * H + h) * kHeadDim + ks * 32 + 8 * g);
       qf[qt][ks] = as_bf16x8(v);
     }
   }
@@ -193,7 +206,7 @@ attn_paged_kernel(const AttnParams P) {
   for (int k0 = kb; k0 < ke; k0 += kChunk) {
     if (k0 + kChunk < ke) load_chunk(k0 + kChunk, kn, vn);
     const bool tail = k0 + kChunk > kvl;
-    const int diag0 = kvl - bl;  // causal: query q may see keys <= diag0 + q
+    const int diag0 = kvl - qc;  // causal: query q may see keys <= diag0 + q
     const bool mask_chunk = tail || (P.causal && k0 + kChunk > diag0 + 1);
     if (tail) {
       // Keys past kv_len contribute P = 0; clear their V too so stale or
@@ -278,8 +291,8 @@ attn_paged_kernel(const AttnParams P) {
   for (int qt = 0; qt < NQT; ++qt) {
     const float L = sum_xor16_32(l[qt]);
     const int q = qt * 16 + n;
-    if (q >= bl) continue;
-    const int64_t row_q = (static_cast<int64_t>(r) * bl + q) * H + h;
+    if (q >= qc) continue;
+    const int64_t row_q = (static_cast<int64_t>(qs) + q) * H + h;
     if (slot < 0) {
       // L = 0 only for a query that sees no key at all (an empty row): zeros, not NaN
       const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -312,9 +325,13 @@ struct MergeParams {
   int bl, H;
   int n_slots;  // parts outside [0, n_slots) are skipped
   uint16_t* out;
+  const int32_t* q_start;  // packed queries, as in AttnParams
+  int n_q;
 };
 
 __device__ __forceinline__ void merge_one(const MergeParams& P, int3 mi, int q) {
+  const int2 rq = row_queries(P.q_start, P.n_q, mi.x, P.bl);
+  if (q >= rq.y) return;
   mi.y = max(mi.y, 0);
   mi.z = max(min(mi.z, P.n_slots - mi.y), 0);  // a merge record past the partials reads nothing
   for (int t = threadIdx.x; t < P.H * 16; t += blockDim.x) {
@@ -339,7 +356,7 @@ __device__ __forceinline__ void merge_one(const MergeParams& P, int3 mi, int q) 
     u32x2_t w2;
     w2[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
     w2[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-    *reinterpret_cast<u32x2_t*>(P.out + ((static_cast<int64_t>(mi.x) * P.bl + q) * P.H + h) * kHeadDim + d0) = w2;
+    *reinterpret_cast<u32x2_t*>(P.out + ((static_cast<int64_t>(rq.x) + q) * P.H + h) * kHeadDim + d0) = w2;
   }
 }
 
@@ -498,7 +515,7 @@ int attn_checks(const void* q, const void* kv_pool, int64_t n_pages, const int32
 int attn_launch(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride,
                 int table_cols, const int32_t* kv_len, int rows, int bl, int n_heads, const int32_t* work, int n_work,
                 const int32_t* merge, int n_merge, const int32_t* counts, float* part_o, float* part_ml, int n_slots,
-                float scale, int causal, void* out, void* stream) {
+                float scale, int causal, void* out, void* stream, const int32_t* q_start, int n_q) {
   yapd::AttnParams P;
   P.q = static_cast<const uint16_t*>(q);
   P.pool = static_cast<const uint16_t*>(kv_pool);
@@ -518,6 +535,8 @@ int attn_launch(const void* q, const void* kv_pool, int64_t n_pages, const int32
   P.scale_log2 = scale * 1.4426950408889634f;
   P.causal = causal != 0;
   P.out = static_cast<uint16_t*>(out);
+  P.q_start = q_start;
+  P.n_q = n_q;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(n_work * (n_heads / yapd::kWaves)), block(64 * yapd::kWaves);
   switch ((bl + 15) / 16) {
@@ -528,7 +547,8 @@ int attn_launch(const void* q, const void* kv_pool, int64_t n_pages, const int32
   }
   YAPD_LAUNCH_CHECK("attn_paged_kernel launch");
   if (n_merge > 0) {
-    yapd::MergeParams M{merge, counts, part_o, part_ml, bl, n_heads, P.n_slots, static_cast<uint16_t*>(out)};
+    yapd::MergeParams M{merge, counts, part_o, part_ml, bl, n_heads, P.n_slots, static_cast<uint16_t*>(out), q_start,
+                        n_q};
     const int64_t pairs = static_cast<int64_t>(n_merge) * bl;
     const dim3 mgrid(static_cast<unsigned>(pairs < yapd::kMergeGrid ? pairs : yapd::kMergeGrid));
     hipLaunchKernelGGL(yapd::attn_merge_kernel, mgrid, dim3(256), 0, st, M, n_merge);

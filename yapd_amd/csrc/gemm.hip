@@ -32,6 +32,7 @@
 // (engines/flashinfer.py:1452-1461).
 #include "common.h"
 #include "kv_layout.h"
+#include "packed.h"
 
 namespace yapd {
 namespace {
@@ -78,6 +79,11 @@ struct GemmParams {
   int64_t n_pages;
   const int32_t* table;
   int table_stride, table_cols;
+  // packed rows (NULL: row m / bl, slot m % bl): token m belongs to row
+  // tok_row[m] of n_rows and sits at slot m - row_start[row] of it
+  const int32_t* tok_row;
+  const int32_t* row_start;
+  int n_rows;
   // affine-quantised W (MLX layout): uint32-packed codes [N, K*bits/32],
   // fp16 scale and bias per (row, 64-column group) [N, K/64]
   const uint32_t* Wq;
@@ -111,8 +117,15 @@ __device__ __forceinline__ RowMeta qkv_row_meta(const GemmParams& p, int m0, int
   RowMeta rm{0, 0};
   if (row < T::BM) {
     const int m = min(m0 + row, p.M - 1);
-    const int r = m / p.bl;
-    const int pos = p.pos0[r] + (m - r * p.bl);
+    int r, slot;
+    if (p.tok_row != nullptr) {
+      r = min(max(p.tok_row[m], 0), p.n_rows - 1);
+      slot = m - p.row_start[r];
+    } else {
+      r = m / p.bl;
+      slot = m - r * p.bl;
+    }
+    const int pos = p.pos0[r] + slot;
     const int pi = min(max(pos, 0) / kPageSize, p.table_cols - 1);
     int64_t page = p.table[static_cast<int64_t>(r) * p.table_stride + pi];
     page = min(max(page, int64_t{0}), p.n_pages - 1);
@@ -1378,6 +1391,24 @@ int rmsnorm_launch(const void* delta, void* residual, const void* x, const void*
   return YAPD_OK;
 }
 }  // namespace
+
+// The QKV + RoPE + KV-write GEMM over packed rows (declared in packed.h).
+int gemm_qkv_rope_kv_packed(const void* A, int64_t lda, const void* W_qkv, int n_tokens, int K, int n_heads,
+                            const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int rows,
+                            const int32_t* row_start, const int32_t* tok_row, void* q_out, void* kv_pool,
+                            int64_t n_pages, const int32_t* page_table, int table_stride, int table_cols,
+                            hipStream_t stream) {
+  YAPD_REQUIRE(row_start && tok_row && rows >= 1, "gemm_qkv packed: NULL row map or no rows");
+  GemmParams p;
+  if (int rc = qkv_params(p, A, lda, W_qkv, n_tokens, K, n_heads, cos_t, sin_t, max_pos, pos0, 1, q_out, kv_pool,
+                          n_pages, page_table, table_stride, table_cols))
+    return rc;
+  p.tok_row = tok_row;
+  p.row_start = row_start;
+  p.n_rows = rows;
+  return launch_gemm<kEpiQkv, kAPlain>(p, stream);
+}
+
 }  // namespace yapd
 
 extern "C" int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,

@@ -8,7 +8,9 @@
 //             adding into the residual -> post-attention RMSNorm ->
 //             gate/up+SiLU GEMM -> down GEMM adding into the residual ->
 //             next input RMSNorm (final norm after the last layer).
+#include "attention.h"
 #include "common.h"
+#include "packed.h"
 
 #define YAPD_TRY(expr)            \
   do {                            \
@@ -16,20 +18,24 @@
     if (_rc != YAPD_OK) return _rc; \
   } while (0)
 
-extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* block_emb,
-                                     int rows, int bl, const int32_t* pos0, const int32_t* kv_len, int causal,
-                                     void* hidden_out, const void* head_w, int vocab, const void* shift_ctx,
-                                     void* logits, int64_t ld_logits, void* stream) {
-  YAPD_REQUIRE(m && ws && block_emb && pos0 && kv_len && hidden_out, "t3_block_forward: NULL pointer");
+namespace {
+
+// Rows of a packed prefill chunk (NULL in a block step): row r's tokens are
+// rows [row_start[r], row_start[r+1]) of the activations, tok_row names each
+// token's row.
+struct PackedRows {
+  const int32_t* row_start;
+  const int32_t* tok_row;
+};
+
+// The shape rules of every per-layer call, checked before the first launch,
+// so that a rejected call leaves the residual, the KV pools and the outputs
+// untouched (the calls below check them again).
+int model_checks(const yapd_t3_model* m, const yapd_t3_workspace* ws) {
   YAPD_REQUIRE(m->n_layers >= 1 && m->layers, "t3_block_forward: no layers");
-  YAPD_REQUIRE(rows >= 1 && bl >= 1 && bl <= 64, "t3_block_forward: need rows >= 1, 1 <= bl <= 64");
   YAPD_REQUIRE(ws->residual && ws->q && ws->attn && ws->normed && ws->delta && ws->act && ws->work,
                "t3_block_forward: incomplete workspace");
-  const int D = m->hidden, H = m->n_heads, F = m->ffn, HD = H * 64;
-  const int M = rows * bl;
-  // The shape rules of every per-layer call, checked before the first launch,
-  // so that a rejected call leaves the residual, the KV pools and the outputs
-  // untouched (the calls below check them again).
+  const int D = m->hidden, H = m->n_heads, F = m->ffn;
   YAPD_REQUIRE(D % 512 == 0 && D >= 512 && D <= 2048, "t3_block_forward: hidden must be 512, 1024, 1536 or 2048 (got %d)",
                D);
   // attention covers 4 heads per workgroup
@@ -46,21 +52,38 @@ extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_works
   }
   YAPD_REQUIRE(ws->n_work >= 1 && (ws->n_merge == 0 || (ws->merge && ws->part_o && ws->part_ml && ws->n_slots >= 1)),
                "t3_block_forward: bad attention plan in the workspace");
-  YAPD_REQUIRE(!head_w || (shift_ctx && logits && vocab >= 1 && ld_logits >= vocab),
-               "t3_block_forward: head needs shift_ctx, logits, vocab >= 1 and ld_logits >= vocab");
+  return YAPD_OK;
+}
+
+// The layer loop over M activation rows (rows x bl, or a packed chunk's
+// tokens), ending in the final norm into hidden_out.
+int run_layers(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* emb, int M, int rows, int bl,
+               const int32_t* pos0, const int32_t* kv_len, int causal, const PackedRows* pk, void* hidden_out,
+               void* st) {
+  const int D = m->hidden, H = m->n_heads, F = m->ffn, HD = H * 64;
   const float scale = 0.125f;  // head_dim ** -0.5 for head_dim 64
-  void* st = stream;
   auto* res = ws->residual;
   auto* xn = ws->normed;
-
-  YAPD_TRY(yapd_rmsnorm(nullptr, res, block_emb, m->layers[0].ln_in, m->layers[0].eps_in, M, D, xn, st));
+  YAPD_TRY(yapd_rmsnorm(nullptr, res, emb, m->layers[0].ln_in, m->layers[0].eps_in, M, D, xn, st));
   for (int li = 0; li < m->n_layers; ++li) {
     const yapd_t3_layer& L = m->layers[li];
-    YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0, bl,
-                                   ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, st));
-    YAPD_TRY(yapd_attn_paged_block(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols,
-                                   kv_len, rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts,
-                                   ws->part_o, ws->part_ml, ws->n_slots, scale, causal, ws->attn, st));
+    if (pk == nullptr) {
+      YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0, bl,
+                                     ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, st));
+      YAPD_TRY(yapd_attn_paged_block(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols,
+                                     kv_len, rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts,
+                                     ws->part_o, ws->part_ml, ws->n_slots, scale, causal, ws->attn, st));
+    } else {
+      YAPD_TRY(yapd::gemm_qkv_rope_kv_packed(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions,
+                                             pos0, rows, pk->row_start, pk->tok_row, ws->q, L.kv_pool, m->n_pages,
+                                             m->page_table, m->table_stride, m->table_cols,
+                                             static_cast<hipStream_t>(st)));
+      YAPD_TRY(yapd::attn_checks(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, kv_len,
+                                 rows, bl, H, ws->work, ws->n_work, ws->attn));
+      YAPD_TRY(yapd::attn_launch(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, kv_len,
+                                 rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts, ws->part_o,
+                                 ws->part_ml, ws->n_slots, scale, causal, ws->attn, st, pk->row_start, M));
+    }
     YAPD_TRY(yapd_gemm_bf16_residual(ws->attn, HD, L.w_o, HD, M, D, HD, res, D, st));
     YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, L.ln_post, L.eps_post, M, D, xn, st));
     YAPD_TRY(yapd_gemm_swiglu(xn, D, L.w_gate_up, M, F, D, ws->act, F, st));
@@ -70,8 +93,38 @@ extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_works
     const float eps = last ? m->final_eps : m->layers[li + 1].eps_in;
     YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, wn, eps, M, D, last ? hidden_out : xn, st));
   }
+  return YAPD_OK;
+}
+
+}  // namespace
+
+extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* block_emb,
+                                     int rows, int bl, const int32_t* pos0, const int32_t* kv_len, int causal,
+                                     void* hidden_out, const void* head_w, int vocab, const void* shift_ctx,
+                                     void* logits, int64_t ld_logits, void* stream) {
+  YAPD_REQUIRE(m && ws && block_emb && pos0 && kv_len && hidden_out, "t3_block_forward: NULL pointer");
+  YAPD_REQUIRE(rows >= 1 && bl >= 1 && bl <= 64, "t3_block_forward: need rows >= 1, 1 <= bl <= 64");
+  YAPD_TRY(model_checks(m, ws));
+  YAPD_REQUIRE(!head_w || (shift_ctx && logits && vocab >= 1 && ld_logits >= vocab),
+               "t3_block_forward: head needs shift_ctx, logits, vocab >= 1 and ld_logits >= vocab");
+  YAPD_TRY(run_layers(m, ws, block_emb, rows * bl, rows, bl, pos0, kv_len, causal, nullptr, hidden_out, stream));
   if (head_w != nullptr) {
-    YAPD_TRY(yapd_gemm_head_shift(hidden_out, shift_ctx, rows, bl, D, head_w, D, vocab, logits, ld_logits, st));
+    YAPD_TRY(yapd_gemm_head_shift(hidden_out, shift_ctx, rows, bl, m->hidden, head_w, m->hidden, vocab, logits,
+                                  ld_logits, stream));
   }
   return YAPD_OK;
+}
+
+extern "C" int yapd_t3_prefill_packed(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* tok_emb,
+                                      int n_tokens, int rows, int max_q, const int32_t* row_start,
+                                      const int32_t* tok_row, const int32_t* pos0, const int32_t* kv_len,
+                                      void* hidden_out, void* stream) {
+  YAPD_REQUIRE(m && ws && tok_emb && row_start && tok_row && pos0 && kv_len && hidden_out,
+               "t3_prefill_packed: NULL pointer");
+  YAPD_REQUIRE(rows >= 1 && max_q >= 1 && max_q <= 64 && n_tokens >= 1 &&
+                   static_cast<int64_t>(n_tokens) <= static_cast<int64_t>(rows) * max_q,
+               "t3_prefill_packed: need rows >= 1, 1 <= max_q <= 64, 1 <= n_tokens <= rows * max_q");
+  YAPD_TRY(model_checks(m, ws));
+  const PackedRows pk{row_start, tok_row};
+  return run_layers(m, ws, tok_emb, n_tokens, rows, max_q, pos0, kv_len, 1, &pk, hidden_out, stream);
 }

@@ -25,6 +25,7 @@ import logging
 import math
 from typing import Dict, List, Optional, Tuple, Union
 
+import numpy as np
 import torch
 from torch import Tensor
 
@@ -305,41 +306,45 @@ class HipEngine:
         return sos
 
     def _prefill(self, row0: int, embs: List[Tensor]) -> Tensor:
-        """Causal forward of ragged prefixes in 64-token chunks on batch rows row0..  A chunk
-        runs only the rows whose prefix reaches into it (through a page table gathered for
-        them when they are not all the rows), so ragged batches compute no chunk of padding;
-        a row's last chunk is padded, and its pad tokens only write KV past the prefix
-        (overwritten by later blocks, never attended)."""
+        """Causal forward of ragged prefixes in chunks of up to 64 tokens per row on batch rows
+        row0..  A chunk runs only the rows whose prefix reaches into it (through a page table
+        gathered for them when they are not all the rows), packed: each row contributes its real
+        tokens only, back to back, so a row's last, partial chunk computes no padding
+        (``yapd_t3_prefill_packed``)."""
         n, D = len(embs), self._hidden
-        lps = [int(e.shape[0]) for e in embs]
-        if min(lps) < 1 or max(lps) > self._max_seq_len:
+        lps = np.array([int(e.shape[0]) for e in embs], dtype=np.int64)
+        if lps.min() < 1 or lps.max() > self._max_seq_len:
             raise ValueError("prefix length must be in [1, max_seq_len]")
-        lp_max = max(lps)
         dev, dt = self._device, self._dtype
-        padded = torch.nn.utils.rnn.pad_sequence([e.to(device=dev, dtype=dt) for e in embs], batch_first=True)
+        flat = torch.cat([e.to(device=dev, dtype=dt) for e in embs])  # the rows' tokens back to back
+        offs = np.concatenate([[0], np.cumsum(lps)[:-1]])
         sos = torch.empty(n, 1, D, dtype=dt, device=dev)
-        for c0 in range(0, lp_max, PREFILL_CHUNK):
-            bl = min(PREFILL_CHUNK, lp_max - c0)
-            active = [r for r in range(n) if lps[r] > c0]
+        for c0 in range(0, int(lps.max()), PREFILL_CHUNK):
+            active = np.nonzero(lps > c0)[0]
             na = len(active)
-            buf = self._buffers(na, bl)
+            cnt = np.minimum(PREFILL_CHUNK, lps[active] - c0)
+            row_start = np.concatenate([[0], np.cumsum(cnt)])
+            T = int(row_start[-1])
+            tok_row = np.repeat(np.arange(na), cnt)
+            tok_src = offs[active][tok_row] + c0 + (np.arange(T) - row_start[tok_row])
+            buf = self._buffers(na, PREFILL_CHUNK)
+            torch.index_select(flat, 0, to_device_async(tok_src, torch.long, dev), out=buf.emb[:T])
             table = None
-            if na == n:
-                buf.emb.view(n, bl, D).copy_(padded[:, c0: c0 + bl])
-            else:
-                idx = to_device_async(active, torch.long, dev)
-                buf.emb.view(na, bl, D).copy_(padded[idx, c0: c0 + bl])
-                table = self._kv.table[idx + row0]
+            if na < n:
+                table = self._kv.table[to_device_async(active + row0, torch.long, dev)]
             buf.pos0.fill_(c0)
-            plan = self._plan([c0 + bl] * na, bl)
-            self._run(buf, plan, plan.kv_len, causal=True, row0=row0, table=table)
-            last = [(i, r) for i, r in enumerate(active) if c0 <= lps[r] - 1 < c0 + bl]
-            if last:
-                hid = buf.hidden.view(na, bl, D)
-                dst = to_device_async([r for _, r in last], torch.long, dev)
-                src_row = to_device_async([i for i, _ in last], torch.long, dev)
-                src_pos = to_device_async([lps[r] - 1 - c0 for _, r in last], torch.long, dev)
-                sos[dst, 0] = hid[src_row, src_pos]
+            plan = self._plan([c0 + int(c) for c in cnt], PREFILL_CHUNK)
+            ws = self._workspace(buf, plan)
+            row_start_dev = to_device_async(row_start, torch.int32, dev)
+            tok_row_dev = to_device_async(tok_row, torch.int32, dev)
+            kernels.check(kernels.load_library().yapd_t3_prefill_packed(
+                ctypes.byref(self._descriptor(row0, table)), ctypes.byref(ws), buf.emb.data_ptr(), T, na,
+                PREFILL_CHUNK, row_start_dev.data_ptr(), tok_row_dev.data_ptr(), buf.pos0.data_ptr(),
+                plan.kv_len.data_ptr(), buf.hidden.data_ptr(), kernels.stream_ptr(dev)))
+            ends = np.nonzero(lps[active] - 1 < c0 + PREFILL_CHUNK)[0]  # rows whose last token is here
+            if len(ends):
+                src = row_start[ends] + (lps[active[ends]] - 1 - c0)
+                sos[to_device_async(active[ends], torch.long, dev), 0] = buf.hidden[to_device_async(src, torch.long, dev)]
         return sos
 
     def causal_forward(self, emb: Tensor) -> Tensor:

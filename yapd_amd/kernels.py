@@ -62,6 +62,8 @@ _SIGNATURES = {
                                  c_void, c_void]),
     "yapd_t3_block_forward": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void, c_int, c_void,
                                       c_void, c_int, c_void, c_void, c_i64, c_void]),
+    "yapd_t3_prefill_packed": (c_int, [c_void, c_void, c_void, c_int, c_int, c_int, c_void, c_void, c_void, c_void,
+                                       c_void, c_void]),
     # include/yapd_vocoder.h
     "yapd_snake": (c_int, [c_void, c_void, c_void, c_void, c_i64, c_int, c_i64, c_void]),
     "yapd_residual_bias": (c_int, [c_void, c_void, c_void, c_void, c_i64, c_int, c_i64, c_void]),
