@@ -260,9 +260,12 @@ int yapd_t3_block_forward(const yapd_t3_model* model, const yapd_t3_workspace* w
                           void* hidden_out, const void* head_w, int vocab, const void* shift_ctx, void* logits,
                           int64_t ld_logits, void* stream);
 
-/* One causal chunk of a prefix prefill (engines/flashinfer.py:prefix_forward
+/* One causal step of a prefix prefill (engines/flashinfer.py:prefix_forward
  * :678-854, the chunked causal forward that writes each row's prefix KV)
- * over packed rows: no row is padded to the chunk length.  Row r's tokens
+ * over packed rows: no row is padded to a chunk length.  A "row" here is a
+ * segment of consecutive tokens of one sequence (its own page-table row);
+ * several consecutive segments of one sequence may share a step, since all
+ * keys of the step are written before any is attended.  Row r's tokens
  * are rows [row_start[r], row_start[r+1]) of tok_emb [n_tokens, D] (at most
  * max_q <= 64 per row), at positions pos0[r], pos0[r] + 1, ...; tok_row
  * [n_tokens] names each token's row; kv_len[r] = pos0[r] + the row's token

@@ -1,6 +1,7 @@
-"""Packed prefix prefill (``yapd_t3_prefill_packed``): each chunk runs only the rows' real
-tokens back to back, where a padded chunk would compute a row's last, partial chunk in full.
-Run against the padded form -- the same prefixes in 64-token chunks through the dense block
+"""Packed prefix prefill (``yapd_t3_prefill_packed``): a step runs segments of up to 64
+consecutive tokens of the prefixes back to back -- several segments of one prefix when they fit
+the step's token budget -- where a padded chunk loop computes every active row's chunk in 64
+tokens and a row's last, partial chunk in full.  Run against the padded form -- the same prefixes in 64-token chunks through the dense block
 forward with ``causal=1``, pad tokens zero (engines/flashinfer.py:prefix_forward :678-854) --
 the SOS hidden and every prefix position's K and V must be equal bit for bit: a GEMM row, an
 attention query and a norm row do not depend on the rows computed beside them.  Prefix lengths
@@ -12,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+import yapd_amd.engines.hip as engine_hip
 from yapd_amd.engines.hip import PREFILL_CHUNK, HipEngine
 from yapd_amd.paged import PAGE_SIZE
 from yapd_amd.synthetic import make_t3
@@ -62,8 +64,11 @@ def prefix_kv(eng, lps, layer):
     return torch.cat(ks), torch.cat(vs)
 
 
-@pytest.mark.parametrize("lps", [[1, 63, 64, 65, 130, 200, 17, 128], [1088, 40, 1280, 700]])
-def test_packed_prefill_equals_padded_chunks(dev, lps):
+@pytest.mark.parametrize("lps,budget", [([1, 63, 64, 65, 130, 200, 17, 128], 16384),
+                                        ([1, 63, 64, 65, 130, 200, 17, 128], 150),  # prefixes across steps
+                                        ([1088, 40, 1280, 700], 16384), ([1088, 40, 1280, 700], 1000)])
+def test_packed_prefill_equals_padded_chunks(dev, lps, budget, monkeypatch):
+    monkeypatch.setattr(engine_hip, "PREFILL_TOKENS", budget)
     model = make_t3(n_layers=2, seed=61, device=dev)
     cap = max(lps) + PREFILL_CHUNK
     kw = dict(batch_size=len(lps), page_table_seed=62)

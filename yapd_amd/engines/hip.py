@@ -35,7 +35,11 @@ from ..paged import PAGE_SIZE, AttnPlan, PagedKV, copy_from_host_async, to_devic
 logger = logging.getLogger(__name__)
 
 CacheStarts = Union[int, List[int]]
-PREFILL_CHUNK = 64
+PREFILL_CHUNK = 64      # tokens per prefill segment (the attention kernel's query limit)
+# Tokens per prefill step: 16384 rows fill the o/down GEMM grids in one round of 256 x 256 tiles
+# (the step's own shape); measured on the 512-row prefill: 8192 285.8 ms, 12288 267.6, 16384 241.2,
+# 20480 266.6, 24576 257.8, 32768 241.9, 65536 249.7, 262144 255.3 (64-token chunk steps: 276-280).
+PREFILL_TOKENS = 16384
 
 
 class _Buffers:
@@ -306,45 +310,56 @@ class HipEngine:
         return sos
 
     def _prefill(self, row0: int, embs: List[Tensor]) -> Tensor:
-        """Causal forward of ragged prefixes in chunks of up to 64 tokens per row on batch rows
-        row0..  A chunk runs only the rows whose prefix reaches into it (through a page table
-        gathered for them when they are not all the rows), packed: each row contributes its real
-        tokens only, back to back, so a row's last, partial chunk computes no padding
-        (``yapd_t3_prefill_packed``)."""
+        """Causal forward of ragged prefixes on batch rows row0.. in steps of up to
+        ``PREFILL_TOKENS`` tokens (``yapd_t3_prefill_packed``).  A step's rows are segments of
+        at most 64 consecutive tokens of one prefix (the attention kernel's query limit),
+        packed back to back: the prefixes are cut into segments in order and the segments
+        into steps, so a step may hold several consecutive segments of one prefix -- the QKV
+        launch writes all of the step's keys before the attention launch reads them, and causal
+        masking orders them -- and no token of padding is computed."""
         n, D = len(embs), self._hidden
         lps = np.array([int(e.shape[0]) for e in embs], dtype=np.int64)
         if lps.min() < 1 or lps.max() > self._max_seq_len:
             raise ValueError("prefix length must be in [1, max_seq_len]")
         dev, dt = self._device, self._dtype
-        flat = torch.cat([e.to(device=dev, dtype=dt) for e in embs])  # the rows' tokens back to back
+        flat = torch.cat([e.to(device=dev, dtype=dt) for e in embs])  # the prefixes back to back
         offs = np.concatenate([[0], np.cumsum(lps)[:-1]])
+        # segments in prefix order: (prefix, first position, token count)
+        n_seg = (lps + PREFILL_CHUNK - 1) // PREFILL_CHUNK
+        seg_row = np.repeat(np.arange(n), n_seg)
+        seg_pos = (np.arange(int(n_seg.sum())) - np.repeat(np.cumsum(n_seg) - n_seg, n_seg)) * PREFILL_CHUNK
+        seg_cnt = np.minimum(PREFILL_CHUNK, lps[seg_row] - seg_pos)
+        seg_end = np.cumsum(seg_cnt)
+        # activations for the largest step, in power-of-two row counts so few sizes are cached
+        need = min(PREFILL_TOKENS, int(seg_end[-1]))
+        buf = self._buffers(1 << max(0, math.ceil(math.log2(-(-need // PREFILL_CHUNK)))), PREFILL_CHUNK)
         sos = torch.empty(n, 1, D, dtype=dt, device=dev)
-        for c0 in range(0, int(lps.max()), PREFILL_CHUNK):
-            active = np.nonzero(lps > c0)[0]
-            na = len(active)
-            cnt = np.minimum(PREFILL_CHUNK, lps[active] - c0)
+        s0 = 0
+        while s0 < len(seg_row):
+            # the next segments up to the token budget (at least one)
+            base = seg_end[s0 - 1] if s0 else 0
+            s1 = max(s0 + 1, int(np.searchsorted(seg_end, base + PREFILL_TOKENS, side="right")))
+            rows, pos, cnt = seg_row[s0:s1], seg_pos[s0:s1], seg_cnt[s0:s1]
             row_start = np.concatenate([[0], np.cumsum(cnt)])
             T = int(row_start[-1])
-            tok_row = np.repeat(np.arange(na), cnt)
-            tok_src = offs[active][tok_row] + c0 + (np.arange(T) - row_start[tok_row])
-            buf = self._buffers(na, PREFILL_CHUNK)
+            tok_row = np.repeat(np.arange(s1 - s0), cnt)
+            tok_src = offs[rows][tok_row] + pos[tok_row] + (np.arange(T) - row_start[tok_row])
             torch.index_select(flat, 0, to_device_async(tok_src, torch.long, dev), out=buf.emb[:T])
-            table = None
-            if na < n:
-                table = self._kv.table[to_device_async(active + row0, torch.long, dev)]
-            buf.pos0.fill_(c0)
-            plan = self._plan([c0 + int(c) for c in cnt], PREFILL_CHUNK)
+            table = self._kv.table[to_device_async(rows + row0, torch.long, dev)]
+            pos0 = to_device_async(pos, torch.int32, dev)
+            plan = self._plan([int(p + c) for p, c in zip(pos, cnt)], PREFILL_CHUNK)
             ws = self._workspace(buf, plan)
             row_start_dev = to_device_async(row_start, torch.int32, dev)
             tok_row_dev = to_device_async(tok_row, torch.int32, dev)
             kernels.check(kernels.load_library().yapd_t3_prefill_packed(
-                ctypes.byref(self._descriptor(row0, table)), ctypes.byref(ws), buf.emb.data_ptr(), T, na,
-                PREFILL_CHUNK, row_start_dev.data_ptr(), tok_row_dev.data_ptr(), buf.pos0.data_ptr(),
+                ctypes.byref(self._descriptor(row0, table)), ctypes.byref(ws), buf.emb.data_ptr(), T, s1 - s0,
+                PREFILL_CHUNK, row_start_dev.data_ptr(), tok_row_dev.data_ptr(), pos0.data_ptr(),
                 plan.kv_len.data_ptr(), buf.hidden.data_ptr(), kernels.stream_ptr(dev)))
-            ends = np.nonzero(lps[active] - 1 < c0 + PREFILL_CHUNK)[0]  # rows whose last token is here
-            if len(ends):
-                src = row_start[ends] + (lps[active[ends]] - 1 - c0)
-                sos[to_device_async(active[ends], torch.long, dev), 0] = buf.hidden[to_device_async(src, torch.long, dev)]
+            last = np.nonzero(pos + cnt == lps[rows])[0]  # segments holding a prefix's last token
+            if len(last):
+                src = row_start[last] + cnt[last] - 1
+                sos[to_device_async(rows[last], torch.long, dev), 0] = buf.hidden[to_device_async(src, torch.long, dev)]
+            s0 = s1
         return sos
 
     def causal_forward(self, emb: Tensor) -> Tensor:
