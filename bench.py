@@ -39,7 +39,8 @@ last-stage tensors of a 48-chunk micro-batch of 80-token chunks
 vocoder's chunk stitch on a 48-job batch.
 
 ``--workload prefill`` times the prefix prefill of the step's rows (causal,
-64-token chunks through the paged KV) in prefix tokens per second.
+packed steps of 64-token segments through the paged KV) in prefix tokens per
+second.
 
 ``--workload attn_stress`` instead measures 30 layers of block attention
 back to back over 256 sequences with log-uniform [64, 2048] prefixes, block
@@ -455,9 +456,9 @@ def prefill_flops(lps, L, D):
 def prefill_workload(args, dev):
     """Prefix prefill (HipEngine.prefix_forward, engines/flashinfer.py:678-854 semantics) of the
     step's 512 rows: prefixes U[150, 600] per pair (cond and null rows share the length), 30
-    layers, causal 64-token chunks writing the paged KV.  Algorithmic work: the projections of
-    the real prefix tokens (2 * D * 16,384 flops per token and layer) plus causal attention;
-    padding the engine computes would count against the rate."""
+    layers, causal, in packed steps of 64-token segments writing the paged KV.  Algorithmic work:
+    the projections of the real prefix tokens (2 * D * 16,384 flops per token and layer) plus
+    causal attention; any padding the engine computed would count against the rate."""
     from yapd_amd.engines.hip import HipEngine
     from yapd_amd.synthetic import make_t3, uniform_lengths
     Bp, L, D = args.pairs, args.layers, 1024
