@@ -496,7 +496,7 @@ def prefill_workload(args, dev):
         "metric": "prefix prefill tokens/sec, 30-layer T3, 512 rows", "value": round(tokens / (ms * 1e-3), 1),
         "unit": "prefix tokens/s", "n_gpus": 1, "ms_per_step": round(ms, 3), "higher_is_better": True,
         "dtype": "bf16", "data": "synthetic (seeded random-init T3 weights, N(0,1) prefix embeddings)",
-        "config": {"workload": "prefix prefill (causal 64-token chunks, paged KV)", "rows": len(lps),
+        "config": {"workload": "prefix prefill (causal, packed steps of 64-token segments, paged KV)", "rows": len(lps),
                    "prefix_len": "U[150,600] per pair", "layers": L, "prefix_tokens": tokens,
                    "wall_ms": round(wall, 2)},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -12,8 +12,8 @@ a drop-in next to FlashInferEngine (engines/flashinfer.py:56-1563):
   replays it and returns views of persistent buffers
   (engines/flashinfer.py:1477-1563);
 * ``prefix_forward`` prefills the conditioning prefix with the same kernels,
-  causal inside 64-token chunks (engines/flashinfer.py:678-854 does it with
-  a ragged FlashInfer prefill).
+  causally, in packed steps of 64-token segments (engines/flashinfer.py:678-854
+  does it with a ragged FlashInfer prefill).
 
 Only bf16 is supported (the deployed dtype); other dtypes raise ValueError.
 """
