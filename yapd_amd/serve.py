@@ -86,18 +86,23 @@ class _AsyncPlan:
         self.rows, self.bl, self.target = rows, bl, target_items
         cap = rows + target_items
         self.cap = cap
-        self.work = torch.zeros(cap, 4, dtype=torch.int32, device=device)
-        self.merge = torch.zeros(rows, 3, dtype=torch.int32, device=device)
-        self.counts = torch.zeros(2, dtype=torch.int32, device=device)
+        # work items, merge records and the two counts in one device block, filled by one copy
+        self._n = cap * 4 + rows * 3 + 2
+        self._blob = torch.zeros(self._n, dtype=torch.int32, device=device)
+        self.work, self.merge, self.counts = self._views(self._blob)
         self.n_slots = cap
         self.part_o = torch.empty(cap, bl, n_heads, 64, dtype=torch.float32, device=device)
         self.part_ml = torch.empty(cap, bl, n_heads, 2, dtype=torch.float32, device=device)
-        self._stage = [(torch.zeros(cap, 4, dtype=torch.int32).pin_memory(),
-                        torch.zeros(rows, 3, dtype=torch.int32).pin_memory(),
-                        torch.zeros(2, dtype=torch.int32).pin_memory()) for _ in range(depth)]
+        self._stage = [torch.zeros(self._n, dtype=torch.int32).pin_memory() for _ in range(depth)]
         self._events: List[Optional[torch.cuda.Event]] = [None] * depth
         self._next = 0
         self.n_merge_live = 0  # split rows of the current plan (0: the merge launch is left out)
+
+    def _views(self, blob: torch.Tensor):
+        """(work [cap, 4], merge [rows, 3], counts [2]) inside one int32 block."""
+        w_end = self.cap * 4
+        m_end = w_end + self.rows * 3
+        return blob[:w_end].view(self.cap, 4), blob[w_end:m_end].view(self.rows, 3), blob[m_end:m_end + 2]
 
     def update(self, kv_upper: List[int]) -> None:
         work, merge, n_slots = kernels.attn_plan(kv_upper, target_items=self.target)
@@ -108,15 +113,13 @@ class _AsyncPlan:
         self._next = (i + 1) % len(self._stage)
         if self._events[i] is not None:
             self._events[i].synchronize()  # issued `depth` ticks ago
-        w, m, c = self._stage[i]
+        blob = self._stage[i]
+        w, m, c = self._views(blob)
         w.numpy()[: work.shape[0]] = work
         if merge.shape[0]:
             m.numpy()[: merge.shape[0]] = merge
         c.numpy()[:] = (work.shape[0], merge.shape[0])
-        self.work[: work.shape[0]].copy_(w[: work.shape[0]], non_blocking=True)
-        if merge.shape[0]:
-            self.merge[: merge.shape[0]].copy_(m[: merge.shape[0]], non_blocking=True)
-        self.counts.copy_(c, non_blocking=True)
+        self._blob.copy_(blob, non_blocking=True)  # one copy of the whole block (a few KB)
         ev = torch.cuda.Event()
         ev.record()
         self._events[i] = ev
