@@ -105,3 +105,23 @@ def test_packed_prefill_of_a_row_subset(dev):
     assert torch.equal(sos, sos_ref)
     for t, b in zip(other, before):
         assert torch.equal(eng._kv.pools[0][torch.as_tensor(t, dtype=torch.long, device=dev)], b)
+
+
+def test_prefixes_filling_the_row_capacity(dev):
+    """A prefix as long as the engine's max_seq_len (the row's last page partly used) and a
+    one-token prefix beside it: same SOS and prefix KV as the padded form."""
+    model = make_t3(n_layers=1, seed=68, device=dev)
+    lps = [200, 1, 199]
+    kw = dict(batch_size=len(lps), page_table_seed=69)
+    eng_p, eng_d = HipEngine(model, 200, torch.bfloat16, **kw), HipEngine(model, 200, torch.bfloat16, **kw)
+    g = torch.Generator().manual_seed(70)
+    embs = [torch.randn(lp, D, generator=g).bfloat16().to(dev) for lp in lps]
+    sos_p = eng_p.prefix_forward(embs)
+    sos_d = padded_prefill(eng_d, embs, dev)
+    torch.cuda.synchronize()
+    assert torch.equal(sos_p, sos_d)
+    kp, vp = prefix_kv(eng_p, lps, 0)
+    kd, vd = prefix_kv(eng_d, lps, 0)
+    assert torch.equal(kp, kd) and torch.equal(vp, vd)
+    with pytest.raises(ValueError):
+        eng_p.prefix_forward([e[:1] for e in embs[:2]] + [torch.zeros(201, D, dtype=torch.bfloat16, device=dev)])
