@@ -54,7 +54,7 @@ struct AttnParams {
   int n_slots;          // partials exist for slots [0, n_slots); an item naming another slot writes nothing
   float scale_log2;     // softmax scale * log2(e)
   int causal;           // 1: query i of the block sees keys < kv_len - n_q(row) + i + 1 (prefix prefill)
-  uint16_t* out;        // [rows, bl, H, 64]
+  uint16_t* out;        // [rows, bl, H, 64] (packed: [n_q, H, 64])
   // Packed queries (NULL: row r's bl queries are rows r*bl ..): row r's queries
   // are q / out rows [q_start[r], q_start[r+1]) of n_q, at most bl of them.
   const int32_t* q_start;
