@@ -27,16 +27,21 @@ def rel_err(out, ref):
 # path: >= 256 output tiles, M not a multiple of 256 in two of them.  M = 3072, N = 1024 is a grid of
 # one 128 x 128 tile per CU, which runs three LDS stages: K = 64 / 128 / 192 give one, two and three
 # k-tiles (the stage hand-off's short and tail cases); (3000, 1000, 4096) a ragged grid of that kind.
+# Grids of at least two 256 x 256 tiles per CU take the persistent kernel: (4100, 8192, 1024) with a
+# partial last row tile, (8000, 4196, 128) with a 100-column last tile and the shortest K it takes (four
+# 32-wide k-tiles: no steady-state iteration after the first), (8192, 8194, 192) with the 2-column tail
+# split off to its own launch.
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 3072, 1024), (1024, 1024, 4096), (37, 8194, 1024),
                                    (16384 // 8, 8192, 1024), (2000, 8192, 1024), (4100, 4096, 2048),
-                                   (3072, 1024, 64), (3072, 1024, 128), (3072, 1024, 192), (3000, 1000, 4096)])
+                                   (3072, 1024, 64), (3072, 1024, 128), (3072, 1024, 192), (3000, 1000, 4096),
+                                   (4100, 8192, 1024), (8000, 4196, 128), (8192, 8194, 192)])
 def test_gemm_bf16(dev, M, N, K):
     A = rnd(M, K, seed=1)
     W = rnd(N, K, std=0.02, seed=2)
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     kernels.gemm_bf16(A.to(dev), W.to(dev), out)
-    ref = A.float() @ W.float().T
-    assert rel_err(out.cpu(), ref) <= 8e-3
+    ref = A.to(dev).float() @ W.to(dev).float().T
+    assert rel_err(out, ref) <= 8e-3
 
 
 # (16384, 1000, 1024): 256 x 256 tiles with a partial last column tile
@@ -69,21 +74,25 @@ def test_gemm_padded_ldc_and_strided_a(dev):
 
 
 @pytest.mark.parametrize("M,K,Fd", [(300, 1024, 4096), (2000, 1024, 4096),  # 2000: large tiles, one round
-                                     (4100, 1024, 4096), (4100, 256, 4096),  # several rounds; ragged M; K < 16 k-tiles
-                                     (8192, 1024, 1088)])  # large tiles, the last one half past 2F
+                                     (4100, 1024, 4096), (4100, 256, 4096),  # persistent; ragged M; K < 16 k-tiles
+                                     (8192, 1024, 1088),  # large tiles, the last one half past 2F
+                                     (16384, 1024, 1088)])  # persistent, the last column tile half past 2F
 def test_gemm_swiglu(dev, M, K, Fd):
     A = rnd(M, K, seed=5)
     Wg = rnd(Fd, K, std=0.02, seed=6)
     Wu = rnd(Fd, K, std=0.02, seed=7)
     act = torch.empty(M, Fd, dtype=torch.bfloat16, device=dev)
     kernels.gemm_swiglu(A.to(dev), kernels.interleave_gate_up(Wg, Wu).to(dev), act)
+    A, Wg, Wu = A.to(dev), Wg.to(dev), Wu.to(dev)
     g = (A.float() @ Wg.float().T).bfloat16()
     u = (A.float() @ Wu.float().T).bfloat16()
     ref = (F.silu(g.float()).bfloat16().float() * u.float()).bfloat16()
-    assert rel_err(act.cpu(), ref.float()) <= 1.5e-2
+    assert rel_err(act, ref.float()) <= 1.5e-2
 
 
-@pytest.mark.parametrize("rows", [6, 70, 64])  # 70 x 32 rows: large tiles; 64 x 32: the 2 last columns split off
+# 70 x 32 rows: large tiles; 64 x 32: the 2 last columns split off; 300 x 32 and 512 x 32 (the step's
+# shape): the persistent kernel and the split-off tail, 300 x 32 with a partial last row tile
+@pytest.mark.parametrize("rows", [6, 70, 64, 300, 512])
 def test_gemm_head_shift(dev, rows):
     bl, D, V = 32, 1024, 8194
     hidden = rnd(rows, bl, D, seed=8)
@@ -91,8 +100,8 @@ def test_gemm_head_shift(dev, rows):
     W = rnd(V, D, std=0.02, seed=10)
     logits = torch.empty(rows, bl, 8200, dtype=torch.bfloat16, device=dev)[..., :V]
     kernels.gemm_head_shift(hidden.to(dev), ctx.to(dev), W.to(dev), logits)
-    ref = OL.speech_head_shift(hidden.float(), ctx.float(), W.float())
-    assert rel_err(logits.cpu(), ref) <= 8e-3
+    ref = OL.speech_head_shift(hidden.to(dev).float(), ctx.to(dev).float(), W.to(dev).float())
+    assert rel_err(logits, ref) <= 8e-3
 
 
 # 180 x 32 rows: large-tile path.  6 heads at 320 x 32 rows: 256-column tiles
