@@ -168,7 +168,8 @@ def main():
     B = 2 * Bp
     D, H, F, V = 1024, 16, 4096, 8194
     t0 = time.time()
-    model = make_t3(n_layers=L, seed=args.seed, device=dev)
+    # the deployed T3's speech embedding adds a learned position table (model.py:397-402)
+    model = make_t3(n_layers=L, seed=args.seed, device=dev, learned_pos_emb=True)
     lens = uniform_lengths(Bp, 150, 600, seed=args.seed + 1)
     lps = lens + lens  # stacked rows: cond 0..Bp-1, null Bp..2Bp-1
     max_seq = max(lps) + 2 * bl
@@ -462,7 +463,8 @@ def prefill_workload(args, dev):
     from yapd_amd.engines.hip import HipEngine
     from yapd_amd.synthetic import make_t3, uniform_lengths
     Bp, L, D = args.pairs, args.layers, 1024
-    model = make_t3(n_layers=L, seed=args.seed, device=dev)
+    # the deployed T3's speech embedding adds a learned position table (model.py:397-402)
+    model = make_t3(n_layers=L, seed=args.seed, device=dev, learned_pos_emb=True)
     lens = uniform_lengths(Bp, 150, 600, seed=args.seed + 1)
     lps = lens + lens
     eng = HipEngine(model, max(lps) + 64, torch.bfloat16, batch_size=len(lps), page_table_seed=args.seed + 2)

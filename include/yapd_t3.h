@@ -206,6 +206,15 @@ int yapd_qgemm_affine(const void* A, int64_t lda, const uint32_t* w_packed, cons
  * final norm (engines/flashinfer.py:_block_forward_fused :970-1065 /
  * _graph_body :1312-1461), optionally followed by the token-shifted head.
  * ------------------------------------------------------------------------ */
+/* One affine-quantised projection weight in the MLX layout (as
+ * yapd_qgemm_affine): packed uint32 [N, K*bits/32], LSB-first codes; scales
+ * and biases fp16 [N, K/64]. */
+typedef struct yapd_t3_qweight {
+  const uint32_t* packed;
+  const void* scales;
+  const void* biases;
+} yapd_t3_qweight;
+
 typedef struct yapd_t3_layer {
   const void* w_qkv;     /* bf16 [3*H*64, D]: q, k, v rows */
   const void* w_o;       /* bf16 [D, H*64] */
@@ -215,6 +224,16 @@ typedef struct yapd_t3_layer {
   const void* ln_post;   /* bf16 [D] */
   float eps_in, eps_post;
   void* kv_pool;         /* this layer's pool */
+  /* Weight-only quantisation of the layer's projections, as the reference's
+   * Metal engine applies to its whole LLaMA stack when
+   * CHATTERBOX_FLASH_MLX_QUANT_BITS is set (engines/mlx.py:221-255):
+   * qbits = 4 or 8 runs the four projections on q_* (same row orders as the
+   * bf16 weights; w_qkv .. w_down are then unused and may be NULL); qbits = 0
+   * runs the bf16 weights.  The fused epilogues are the same, and the result
+   * equals the bf16 path's on the dequantised weights bf16(scale*q + bias)
+   * bit for bit. */
+  int qbits;
+  yapd_t3_qweight q_qkv, q_o, q_gate_up, q_down;
 } yapd_t3_layer;
 
 typedef struct yapd_t3_model {

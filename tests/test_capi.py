@@ -186,6 +186,39 @@ def test_packed_prefill_checks_before_launching(n_tokens, rows, max_q, msg):
     assert rc == EINVAL and b"NULL pointer" in lib.yapd_last_error()
 
 
+def test_block_forward_checks_alignment_and_quant_layers_before_launching():
+    """Misaligned workspace or partials pointers and bad quantised layers are
+    refused by the up-front checks (EINVAL here, where no launch could run:
+    the checks come before any launch, so nothing is modified)."""
+    lib = kernels.load_library()
+
+    def call(model, ws):
+        return lib.yapd_t3_block_forward(ctypes.byref(model), ctypes.byref(ws), P, 4, 32, P, P, 0, P, None, 0, None,
+                                         None, 0, None)
+    model, ws, _keep = _block_forward_args()
+    ws.q = P + 4
+    assert call(model, ws) == EINVAL and b"16-byte aligned" in lib.yapd_last_error()
+    model, ws, _keep = _block_forward_args()
+    ws.work = P + 8
+    assert call(model, ws) == EINVAL and b"16-byte aligned" in lib.yapd_last_error()
+    model, ws, _keep = _block_forward_args()
+    ws.merge, ws.n_merge, ws.part_o, ws.part_ml, ws.n_slots = P, 2, P + 4, P, 4
+    assert call(model, ws) == EINVAL and b"part_o must be 16-byte aligned" in lib.yapd_last_error()
+    rc = lib.yapd_t3_prefill_packed(ctypes.byref(model), ctypes.byref(ws), P, 10, 4, 64, P, P, P, P, P, None)
+    assert rc == EINVAL and b"part_o must be 16-byte aligned" in lib.yapd_last_error()
+    model, ws, layers = _block_forward_args()
+    layers[1].qbits = 3
+    assert call(model, ws) == EINVAL and b"bits must be 4 or 8" in lib.yapd_last_error()
+    layers[1].qbits = 4
+    assert call(model, ws) == EINVAL and b"NULL quantised weight" in lib.yapd_last_error()
+    # (never a fully valid layer set: these pointers are not device memory)
+    for name in ("q_qkv", "q_o", "q_gate_up"):
+        setattr(layers[1], name, kernels.T3QWeight(P, P, P))
+    layers[1].w_qkv = None  # unused by a quantised layer: the next rule is the one reported
+    layers[1].q_down = kernels.T3QWeight(P + 4, P, P)
+    assert call(model, ws) == EINVAL and b"q_down: packed weights must be 16-byte aligned" in lib.yapd_last_error()
+
+
 def test_block_forward_rejects_incomplete_layer_and_head():
     lib = kernels.load_library()
     model, ws, layers = _block_forward_args()

@@ -55,3 +55,21 @@ def test_quant_rows_do_not_depend_on_batch_size(dev, bits):
     outs = [qgemm_affine(A[:M], packed, s, b, bits).cpu() for M in (16384, 8192, 1024, 96)]
     for M, out in zip((8192, 1024, 96), outs[1:]):
         assert torch.equal(outs[0][:M], out), M
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("N,K", [(3072, 1024), (1024, 1024), (8192, 1024), (1024, 4096)])
+def test_c5_projection_shapes_at_m8192(dev, bits, N, K):
+    """The benched quantised projections -- QKV, o_proj, gate/up and down of the
+    T3 layer at M = 256 x 32 tokens -- against dequantise-then-matmul in fp32."""
+    M = 8192
+    g = torch.Generator(device=dev).manual_seed(N + K + bits)
+    w = torch.randn(N, K, generator=g, device=dev) * 0.02
+    a = torch.randn(M, K, generator=g, device=dev).bfloat16()
+    packed, s, b = quantize_affine(w, bits)
+    out = qgemm_affine(a, packed, s, b, bits)
+    w_hat = torch.from_numpy(Q.dequantize(packed.cpu().numpy().view(np.uint32), s.cpu().numpy(),
+                                          b.cpu().numpy(), bits)).to(dev)
+    ref = a.float() @ w_hat.T
+    rel = ((out.float() - ref).abs().max() / ref.abs().max()).item()
+    assert rel <= 1e-2, rel

@@ -33,6 +33,7 @@
 #include "common.h"
 #include "kv_layout.h"
 #include "packed.h"
+#include "quant.h"
 
 namespace yapd {
 namespace {
@@ -844,8 +845,10 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dl_kernel(const GemmParams p)
 // chunk (w = scale * q + bias, rounded once to bf16, as in gemm_kernel) and
 // writes it into the next stage's B tile in the same swizzled layout, so the
 // fragment reads and the MFMA loop are gemm_dl_kernel's.  Only W passes
-// through ds_write (half of the register-staged kernel's LDS writes).
-template <class T, int AM, int BQ>
+// through ds_write (half of the register-staged kernel's LDS writes).  The
+// epilogues are gemm_dl_kernel's: a row's result equals the bf16 kernel's on
+// the dequantised weights bit for bit (same W values, MFMA and K order).
+template <class T, int EPI, int AM, int BQ>
 __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p) {
   using L = DlLayout<T, 2>;
   static_assert(BQ == 4 || BQ == 8, "4- or 8-bit codes");
@@ -964,7 +967,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
       for (int j = 0; j < T::TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = EPI == kEpiQkv || EPI == kEpiSwiglu  // transposed product for these epilogues
+                        ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0)
+                        : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
   };
   auto interleave = [&]() {
 #pragma unroll
@@ -974,6 +979,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
     }
     __builtin_amdgcn_sched_group_barrier(0x008, T::TM * T::TN - (T::TM + T::TN), 0);
   };
+  const RowMeta rm = EPI == kEpiQkv ? qkv_row_meta<T>(p, m0, tid) : RowMeta{0, 0};
 
   // Two stages.  Tile kt+1's A is requested and its W codes fetched at the
   // top of tile kt; W is dequantised into the other stage after the k-tile's
@@ -1005,8 +1011,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
     if (more) interleave();
     stage ^= 1;
   }
-  const RowMeta rm{0, 0};
-  finish_tile<T, kEpiStore>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
+  static_assert(EPI != kEpiQkv || qkv_lds_bytes<T>() <= L::LDS, "qkv epilogue LDS");
+  finish_tile<T, EPI>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -1403,21 +1409,21 @@ int launch_dl(const GemmParams& p, hipStream_t st) {
 using TileD = Tile<256, 256, BK, 2, 4>;  // direct-load large tile
 using TileM = Tile<128, 128, BK, 4, 2>;  // direct-load mid tile: 8 waves of 32 x 64
 
-template <class T, int AM, int BQ>
+template <class T, int EPI, int AM, int BQ>
 int launch_dlq(const GemmParams& p, hipStream_t st) {
   using L = DlLayout<T, 2>;
   static bool lds_set[64] = {false};
   int dev = 0;
   if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
   if (dev < 0 || dev >= 64 || !lds_set[dev]) {
-    if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dlq_kernel<T, AM, BQ>),
+    if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dlq_kernel<T, EPI, AM, BQ>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS),
                            "gemm_dlq_kernel LDS attribute"))
       return rc;
     if (dev >= 0 && dev < 64) lds_set[dev] = true;
   }
   const dim3 grid((p.N + T::BN - 1) / T::BN, (p.M + T::BM - 1) / T::BM), block(T::THREADS);
-  hipLaunchKernelGGL((gemm_dlq_kernel<T, AM, BQ>), grid, block, L::LDS, st, p);
+  hipLaunchKernelGGL((gemm_dlq_kernel<T, EPI, AM, BQ>), grid, block, L::LDS, st, p);
   YAPD_LAUNCH_CHECK("gemm_dlq_kernel launch");
   return YAPD_OK;
 }
@@ -1519,8 +1525,7 @@ int launch_gemm(GemmParams p, hipStream_t st) {
       }
       return launch_dl<TileD, EPI, AM>(p, st);
     } else {
-      static_assert(EPI == kEpiStore, "the quantised path stores plainly");
-      return launch_dlq<TileD, AM, BQ>(p, st);
+      return launch_dlq<TileD, EPI, AM, BQ>(p, st);
     }
   }
   // Few tiles (small batches): one-wave 64 x 64 direct-load tiles with two
@@ -1554,7 +1559,7 @@ int launch_gemm(GemmParams p, hipStream_t st) {
     // has at most one tile per CU (M = 256-4096, bit-identical: down 4-bit
     // 58.1 -> 44.7 us at M = 256, 78.0 -> 72.5 us at M = 4096); larger grids
     // keep the register-staged kernel (o at M = 8192: 29.3 vs 32.5 us).
-    if (small_tiles <= cu_count()) return launch_dlq<TileM, AM, BQ>(p, st);
+    if (small_tiles <= cu_count()) return launch_dlq<TileM, EPI, AM, BQ>(p, st);
     return launch_tile<TileS, EPI, AM, BQ>(p, st);
   }
 }
@@ -1648,13 +1653,22 @@ extern "C" int yapd_gemm_swiglu(const void* A, int64_t lda, const void* W_gu_int
 namespace yapd {
 namespace {
 // Parameters and argument checks of the QKV + RoPE + KV-write GEMM (nothing launched).
+// With q != nullptr the weight is quantised (W_qkv unused).
 int qkv_params(GemmParams& p, const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
                const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos0, int bl, void* q_out,
-               void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride, int table_cols) {
+               void* kv_pool, int64_t n_pages, const int32_t* page_table, int table_stride, int table_cols,
+               const QWeight* q = nullptr) {
   p = GemmParams{};
   p.A = static_cast<const uint16_t*>(A);
   p.lda = lda;
-  p.W = static_cast<const uint16_t*>(W_qkv);
+  if (q != nullptr) {
+    p.Wq = q->packed;
+    p.ldq = static_cast<int64_t>(K) * q->bits / 32;
+    p.qscale = q->scales;
+    p.qbias = q->biases;
+  } else {
+    p.W = static_cast<const uint16_t*>(W_qkv);
+  }
   p.ldw = K;
   p.M = M;
   p.N = 3 * n_heads * kHeadDim;
@@ -1716,6 +1730,82 @@ int gemm_qkv_rope_kv_packed(const void* A, int64_t lda, const void* W_qkv, int n
   p.row_start = row_start;
   p.n_rows = rows;
   return launch_gemm<kEpiQkv, kAPlain>(p, stream);
+}
+
+int qweight_checks(const QWeight& w, int N, int K, const char* what) {
+  YAPD_REQUIRE(w.bits == 4 || w.bits == 8, "%s: bits must be 4 or 8 (got %d)", what, w.bits);
+  YAPD_REQUIRE(w.packed && w.scales && w.biases, "%s: NULL quantised weight", what);
+  YAPD_REQUIRE(al16(w.packed), "%s: packed weights must be 16-byte aligned", what);
+  YAPD_REQUIRE(N >= 1 && K >= BK && K % BK == 0, "%s: need N >= 1 and K %% %d == 0", what, BK);
+  return YAPD_OK;
+}
+
+namespace {
+// GemmParams of a quantised projection (A, M, N, K, C set by the caller).
+void set_q(GemmParams& p, const QWeight& w, int K) {
+  p.Wq = w.packed;
+  p.ldq = static_cast<int64_t>(K) * w.bits / 32;
+  p.qscale = w.scales;
+  p.qbias = w.biases;
+}
+
+template <int EPI>
+int launch_q(const GemmParams& p, int bits, hipStream_t st) {
+  return bits == 4 ? launch_gemm<EPI, kAPlain, 4>(p, st) : launch_gemm<EPI, kAPlain, 8>(p, st);
+}
+}  // namespace
+
+int qgemm_residual(const void* A, int64_t lda, const QWeight& w, int M, int N, int K, void* residual, int64_t ld_res,
+                   hipStream_t stream) {
+  if (int rc = qweight_checks(w, N, K, "qgemm_residual")) return rc;
+  GemmParams p{};
+  p.A = static_cast<const uint16_t*>(A);
+  p.lda = lda;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.C = static_cast<uint16_t*>(residual);
+  p.ldc = ld_res;
+  set_q(p, w, K);
+  if (int rc = check_common(p)) return rc;
+  YAPD_REQUIRE(residual != nullptr && ld_res >= N, "qgemm_residual: bad residual");
+  return launch_q<kEpiResidual>(p, w.bits, stream);
+}
+
+int qgemm_swiglu(const void* A, int64_t lda, const QWeight& w, int M, int F, int K, void* act, int64_t ld_act,
+                 hipStream_t stream) {
+  if (int rc = qweight_checks(w, 2 * F, K, "qgemm_swiglu")) return rc;
+  GemmParams p{};
+  p.A = static_cast<const uint16_t*>(A);
+  p.lda = lda;
+  p.M = M;
+  p.N = 2 * F;
+  p.K = K;
+  p.C = static_cast<uint16_t*>(act);
+  p.ldc = ld_act;
+  set_q(p, w, K);
+  if (int rc = check_common(p)) return rc;
+  YAPD_REQUIRE(act && F % 64 == 0 && ld_act >= F, "qgemm_swiglu: F must be a multiple of 64");
+  return launch_q<kEpiSwiglu>(p, w.bits, stream);
+}
+
+int qgemm_qkv_rope_kv(const void* A, int64_t lda, const QWeight& w, int M, int K, int n_heads, const float* cos_t,
+                      const float* sin_t, int max_pos, const int32_t* pos0, int bl, int rows, const int32_t* row_start,
+                      const int32_t* tok_row, void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table,
+                      int table_stride, int table_cols, hipStream_t stream) {
+  if (int rc = qweight_checks(w, 3 * n_heads * kHeadDim, K, "qgemm_qkv")) return rc;
+  const bool packed = row_start != nullptr;
+  YAPD_REQUIRE(!packed || (tok_row && rows >= 1), "qgemm_qkv packed: NULL row map or no rows");
+  GemmParams p;
+  if (int rc = qkv_params(p, A, lda, nullptr, M, K, n_heads, cos_t, sin_t, max_pos, pos0, packed ? 1 : bl, q_out,
+                          kv_pool, n_pages, page_table, table_stride, table_cols, &w))
+    return rc;
+  if (packed) {
+    p.tok_row = tok_row;
+    p.row_start = row_start;
+    p.n_rows = rows;
+  }
+  return launch_q<kEpiQkv>(p, w.bits, stream);
 }
 
 }  // namespace yapd

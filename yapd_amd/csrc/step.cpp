@@ -11,6 +11,7 @@
 #include "attention.h"
 #include "common.h"
 #include "packed.h"
+#include "quant.h"
 
 #define YAPD_TRY(expr)            \
   do {                            \
@@ -28,13 +29,25 @@ struct PackedRows {
   const int32_t* tok_row;
 };
 
-// The shape rules of every per-layer call, checked before the first launch,
-// so that a rejected call leaves the residual, the KV pools and the outputs
-// untouched (the calls below check them again).
-int model_checks(const yapd_t3_model* m, const yapd_t3_workspace* ws) {
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+yapd::QWeight qw(const yapd_t3_qweight& w, int bits) {
+  return yapd::QWeight{w.packed, static_cast<const uint16_t*>(w.scales), static_cast<const uint16_t*>(w.biases),
+                       bits};
+}
+
+// The rules of every per-layer call (shapes, pointers, alignment, the
+// attention plan), checked before the first launch, so that a rejected call
+// leaves the residual, the KV pools and the outputs untouched (the calls below
+// check them again).
+int model_checks(const yapd_t3_model* m, const yapd_t3_workspace* ws, int rows, int bl, const int32_t* pos0,
+                 const int32_t* kv_len) {
   YAPD_REQUIRE(m->n_layers >= 1 && m->layers, "t3_block_forward: no layers");
   YAPD_REQUIRE(ws->residual && ws->q && ws->attn && ws->normed && ws->delta && ws->act && ws->work,
                "t3_block_forward: incomplete workspace");
+  YAPD_REQUIRE(al16(ws->residual) && al16(ws->q) && al16(ws->attn) && al16(ws->normed) && al16(ws->delta) &&
+                   al16(ws->act),
+               "t3_block_forward: workspace activations must be 16-byte aligned");
   const int D = m->hidden, H = m->n_heads, F = m->ffn;
   YAPD_REQUIRE(D % 512 == 0 && D >= 512 && D <= 2048, "t3_block_forward: hidden must be 512, 1024, 1536 or 2048 (got %d)",
                D);
@@ -43,15 +56,32 @@ int model_checks(const yapd_t3_model* m, const yapd_t3_workspace* ws) {
   YAPD_REQUIRE(F % 64 == 0 && F >= 64, "t3_block_forward: ffn must be a multiple of 64 (got %d)", F);
   YAPD_REQUIRE(m->rope_cos && m->rope_sin && m->rope_positions >= 1 && m->final_norm,
                "t3_block_forward: missing RoPE tables or final norm");
-  YAPD_REQUIRE(m->page_table && m->n_pages >= 1 && m->table_cols >= 1 && m->table_stride >= m->table_cols,
+  YAPD_REQUIRE(al16(m->rope_cos) && al16(m->rope_sin), "t3_block_forward: RoPE tables must be 16-byte aligned");
+  YAPD_REQUIRE(m->page_table && m->n_pages >= 1 && m->n_pages <= INT32_MAX && m->table_cols >= 1 &&
+                   m->table_stride >= m->table_cols,
                "t3_block_forward: bad page table");
+  const int HD = H * 64;
   for (int li = 0; li < m->n_layers; ++li) {
     const yapd_t3_layer& L = m->layers[li];
-    YAPD_REQUIRE(L.w_qkv && L.w_o && L.w_gate_up && L.w_down && L.ln_in && L.ln_post && L.kv_pool,
-                 "t3_block_forward: layer %d has a NULL weight or KV pool", li);
+    YAPD_REQUIRE(L.ln_in && L.ln_post && L.kv_pool, "t3_block_forward: layer %d has a NULL norm or KV pool", li);
+    YAPD_REQUIRE(al16(L.kv_pool), "t3_block_forward: layer %d KV pool must be 16-byte aligned", li);
+    if (L.qbits == 0) {
+      YAPD_REQUIRE(L.w_qkv && L.w_o && L.w_gate_up && L.w_down, "t3_block_forward: layer %d has a NULL weight", li);
+      YAPD_REQUIRE(al16(L.w_qkv) && al16(L.w_o) && al16(L.w_gate_up) && al16(L.w_down),
+                   "t3_block_forward: layer %d weights must be 16-byte aligned", li);
+    } else {
+      YAPD_TRY(yapd::qweight_checks(qw(L.q_qkv, L.qbits), 3 * HD, D, "t3_block_forward q_qkv"));
+      YAPD_TRY(yapd::qweight_checks(qw(L.q_o, L.qbits), D, HD, "t3_block_forward q_o"));
+      YAPD_TRY(yapd::qweight_checks(qw(L.q_gate_up, L.qbits), 2 * F, D, "t3_block_forward q_gate_up"));
+      YAPD_TRY(yapd::qweight_checks(qw(L.q_down, L.qbits), D, F, "t3_block_forward q_down"));
+    }
+    YAPD_TRY(yapd::attn_checks(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, kv_len,
+                               rows, bl, H, ws->work, ws->n_work, ws->attn));
   }
   YAPD_REQUIRE(ws->n_work >= 1 && (ws->n_merge == 0 || (ws->merge && ws->part_o && ws->part_ml && ws->n_slots >= 1)),
                "t3_block_forward: bad attention plan in the workspace");
+  YAPD_REQUIRE(ws->n_merge == 0 || al16(ws->part_o), "t3_block_forward: part_o must be 16-byte aligned");
+  YAPD_REQUIRE(pos0 != nullptr, "t3_block_forward: NULL pos0");
   return YAPD_OK;
 }
 
@@ -65,29 +95,46 @@ int run_layers(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* 
   auto* res = ws->residual;
   auto* xn = ws->normed;
   YAPD_TRY(yapd_rmsnorm(nullptr, res, emb, m->layers[0].ln_in, m->layers[0].eps_in, M, D, xn, st));
+  const hipStream_t hst = static_cast<hipStream_t>(st);
   for (int li = 0; li < m->n_layers; ++li) {
     const yapd_t3_layer& L = m->layers[li];
+    const bool q = L.qbits != 0;
+    if (q) {
+      YAPD_TRY(yapd::qgemm_qkv_rope_kv(xn, D, qw(L.q_qkv, L.qbits), M, D, H, m->rope_cos, m->rope_sin,
+                                       m->rope_positions, pos0, bl, rows, pk ? pk->row_start : nullptr,
+                                       pk ? pk->tok_row : nullptr, ws->q, L.kv_pool, m->n_pages, m->page_table,
+                                       m->table_stride, m->table_cols, hst));
+    }
     if (pk == nullptr) {
-      YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0, bl,
-                                     ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, st));
+      if (!q)
+        YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0,
+                                       bl, ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride,
+                                       m->table_cols, st));
       YAPD_TRY(yapd_attn_paged_block(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols,
                                      kv_len, rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts,
                                      ws->part_o, ws->part_ml, ws->n_slots, scale, causal, ws->attn, st));
     } else {
-      YAPD_TRY(yapd::gemm_qkv_rope_kv_packed(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions,
-                                             pos0, rows, pk->row_start, pk->tok_row, ws->q, L.kv_pool, m->n_pages,
-                                             m->page_table, m->table_stride, m->table_cols,
-                                             static_cast<hipStream_t>(st)));
-      YAPD_TRY(yapd::attn_checks(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, kv_len,
-                                 rows, bl, H, ws->work, ws->n_work, ws->attn));
+      if (!q)
+        YAPD_TRY(yapd::gemm_qkv_rope_kv_packed(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions,
+                                               pos0, rows, pk->row_start, pk->tok_row, ws->q, L.kv_pool, m->n_pages,
+                                               m->page_table, m->table_stride, m->table_cols, hst));
       YAPD_TRY(yapd::attn_launch(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, kv_len,
                                  rows, bl, H, ws->work, ws->n_work, ws->merge, ws->n_merge, ws->counts, ws->part_o,
                                  ws->part_ml, ws->n_slots, scale, causal, ws->attn, st, pk->row_start, M));
     }
-    YAPD_TRY(yapd_gemm_bf16_residual(ws->attn, HD, L.w_o, HD, M, D, HD, res, D, st));
+    if (q) {
+      YAPD_TRY(yapd::qgemm_residual(ws->attn, HD, qw(L.q_o, L.qbits), M, D, HD, res, D, hst));
+    } else {
+      YAPD_TRY(yapd_gemm_bf16_residual(ws->attn, HD, L.w_o, HD, M, D, HD, res, D, st));
+    }
     YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, L.ln_post, L.eps_post, M, D, xn, st));
-    YAPD_TRY(yapd_gemm_swiglu(xn, D, L.w_gate_up, M, F, D, ws->act, F, st));
-    YAPD_TRY(yapd_gemm_bf16_residual(ws->act, F, L.w_down, F, M, D, F, res, D, st));
+    if (q) {
+      YAPD_TRY(yapd::qgemm_swiglu(xn, D, qw(L.q_gate_up, L.qbits), M, F, D, ws->act, F, hst));
+      YAPD_TRY(yapd::qgemm_residual(ws->act, F, qw(L.q_down, L.qbits), M, D, F, res, D, hst));
+    } else {
+      YAPD_TRY(yapd_gemm_swiglu(xn, D, L.w_gate_up, M, F, D, ws->act, F, st));
+      YAPD_TRY(yapd_gemm_bf16_residual(ws->act, F, L.w_down, F, M, D, F, res, D, st));
+    }
     const bool last = li + 1 == m->n_layers;
     const void* wn = last ? m->final_norm : m->layers[li + 1].ln_in;
     const float eps = last ? m->final_eps : m->layers[li + 1].eps_in;
@@ -104,7 +151,7 @@ extern "C" int yapd_t3_block_forward(const yapd_t3_model* m, const yapd_t3_works
                                      void* logits, int64_t ld_logits, void* stream) {
   YAPD_REQUIRE(m && ws && block_emb && pos0 && kv_len && hidden_out, "t3_block_forward: NULL pointer");
   YAPD_REQUIRE(rows >= 1 && bl >= 1 && bl <= 64, "t3_block_forward: need rows >= 1, 1 <= bl <= 64");
-  YAPD_TRY(model_checks(m, ws));
+  YAPD_TRY(model_checks(m, ws, rows, bl, pos0, kv_len));
   YAPD_REQUIRE(!head_w || (shift_ctx && logits && vocab >= 1 && ld_logits >= vocab),
                "t3_block_forward: head needs shift_ctx, logits, vocab >= 1 and ld_logits >= vocab");
   YAPD_TRY(run_layers(m, ws, block_emb, rows * bl, rows, bl, pos0, kv_len, causal, nullptr, hidden_out, stream));
@@ -124,7 +171,7 @@ extern "C" int yapd_t3_prefill_packed(const yapd_t3_model* m, const yapd_t3_work
   YAPD_REQUIRE(rows >= 1 && max_q >= 1 && max_q <= 64 && n_tokens >= 1 &&
                    static_cast<int64_t>(n_tokens) <= static_cast<int64_t>(rows) * max_q,
                "t3_prefill_packed: need rows >= 1, 1 <= max_q <= 64, 1 <= n_tokens <= rows * max_q");
-  YAPD_TRY(model_checks(m, ws));
+  YAPD_TRY(model_checks(m, ws, rows, max_q, pos0, kv_len));
   const PackedRows pk{row_start, tok_row};
   return run_layers(m, ws, tok_emb, n_tokens, rows, max_q, pos0, kv_len, 1, &pk, hidden_out, stream);
 }

@@ -23,6 +23,7 @@ from __future__ import annotations
 import ctypes
 import logging
 import math
+import os
 from typing import Dict, List, Optional, Tuple, Union
 
 import numpy as np
@@ -60,11 +61,35 @@ class _Buffers:
         self.pos0 = torch.zeros(rows, dtype=torch.int32, device=dev)
 
 
+def _quant_bits_from(quant_bits: Optional[int]) -> int:
+    """0 (bf16 weights), 4 or 8.  Unset: ``CHATTERBOX_FLASH_MLX_QUANT_BITS`` (engines/mlx.py:224-240:
+    an unparsable value is ignored with a warning; the group size stays 64)."""
+    if quant_bits is None:
+        raw = os.environ.get("CHATTERBOX_FLASH_MLX_QUANT_BITS", "").strip()
+        if not raw:
+            return 0
+        try:
+            quant_bits = int(raw)
+        except ValueError:
+            logger.warning("Ignoring invalid CHATTERBOX_FLASH_MLX_QUANT_BITS=%r", raw)
+            return 0
+        group = int(os.environ.get("CHATTERBOX_FLASH_MLX_QUANT_GROUP", "64"))
+        if group != 64:
+            raise ValueError(f"HipEngine quantises with group size 64; got CHATTERBOX_FLASH_MLX_QUANT_GROUP={group}")
+    if quant_bits not in (0, 4, 8):
+        raise ValueError(f"HipEngine quantises to 4 or 8 bits; got {quant_bits}")
+    return int(quant_bits)
+
+
 class HipEngine:
     """Paged-KV engine on hand-written gfx950 kernels (``backend="hip"``)."""
 
     def __init__(self, model, max_seq_len: int, dtype: torch.dtype, *, batch_size: int = 1,
-                 page_size: int = 16, page_table_seed: Optional[int] = None, attn_target_items: int = 192):
+                 page_size: int = 16, page_table_seed: Optional[int] = None, attn_target_items: int = 192,
+                 quant_bits: Optional[int] = None):
+        """``quant_bits`` 4 or 8 runs every layer projection on affine group-quantised weights (MLX
+        layout, group 64; engines/mlx.py:221-255); ``None`` takes ``CHATTERBOX_FLASH_MLX_QUANT_BITS``
+        from the environment as the reference's Metal engine does (unset: bf16 weights)."""
         if dtype != torch.bfloat16:
             raise ValueError(f"HipEngine runs bf16 only; got {dtype}")
         if page_size != PAGE_SIZE:
@@ -92,6 +117,7 @@ class HipEngine:
         self._num_heads = H
         self._hidden = D
         self._attn_target = int(attn_target_items)
+        self._quant_bits = _quant_bits_from(quant_bits)
 
         # ---- weights: fused / re-laid-out copies (engines/flashinfer.py:152-187) ----
         self._w: List[Dict[str, Tensor]] = []
@@ -110,6 +136,15 @@ class HipEngine:
             self._final_norm = tf.norm.weight.to(dtype).contiguous()
             self._final_eps = float(tf.norm.variance_epsilon)
             self._ffn = self._w[0]["wd"].shape[1]
+            if self._quant_bits:
+                # Quantise the fused copies row by row (groups of 64 along the input dim,
+                # so fusing and interleaving rows commutes with quantising); the bf16
+                # copies are dropped.
+                from ..quant import quantize_affine
+                for w in self._w:
+                    for key in ("wqkv", "wo", "wgu", "wd"):
+                        w["q_" + key] = quantize_affine(w[key], self._quant_bits)
+                        w[key] = None
             # RoPE table from the model's own rotary embedding (handles llama3
             # scaling; engines/flashinfer.py:195-255), values of the model dtype.
             dummy = torch.zeros(1, 1, D, device=dev, dtype=dtype)
@@ -132,10 +167,16 @@ class HipEngine:
         # ---- native model descriptor ----
         self._c_layers = (kernels.T3Layer * L)()
         for li, w in enumerate(self._w):
-            self._c_layers[li] = kernels.T3Layer(
-                w["wqkv"].data_ptr(), w["wo"].data_ptr(), w["wgu"].data_ptr(), w["wd"].data_ptr(),
+            lay = kernels.T3Layer(
+                kernels.ptr(w["wqkv"]), kernels.ptr(w["wo"]), kernels.ptr(w["wgu"]), kernels.ptr(w["wd"]),
                 w["ln_in"].data_ptr(), w["ln_post"].data_ptr(), w["eps_in"], w["eps_post"],
                 self._kv.pools[li].data_ptr())
+            if self._quant_bits:
+                lay.qbits = self._quant_bits
+                for key, field in (("wqkv", "q_qkv"), ("wo", "q_o"), ("wgu", "q_gate_up"), ("wd", "q_down")):
+                    pk, sc, bi = w["q_" + key]
+                    setattr(lay, field, kernels.T3QWeight(pk.data_ptr(), sc.data_ptr(), bi.data_ptr()))
+            self._c_layers[li] = lay
         self._c_model = kernels.T3Model(
             L, D, H, self._ffn, ctypes.cast(self._c_layers, ctypes.POINTER(kernels.T3Layer)),
             self._final_norm.data_ptr(), self._final_eps, self._cos.data_ptr(), self._sin.data_ptr(),
@@ -166,6 +207,11 @@ class HipEngine:
     @property
     def batch_size(self) -> int:
         return self._batch_size
+
+    @property
+    def quant_bits(self) -> int:
+        """4 or 8 when the layer projections run on quantised weights, else 0."""
+        return self._quant_bits
 
     @property
     def cache_len(self) -> int:

@@ -79,11 +79,17 @@ _SIGNATURES = {
 STITCH_JOB_INTS = 12  # YAPD_STITCH_JOB_INTS of include/yapd_vocoder.h
 
 
+class T3QWeight(ctypes.Structure):
+    """``yapd_t3_qweight`` of include/yapd_t3.h (MLX-layout codes, fp16 scales and biases)."""
+    _fields_ = [("packed", c_void), ("scales", c_void), ("biases", c_void)]
+
+
 class T3Layer(ctypes.Structure):
-    """``yapd_t3_layer`` of include/yapd_t3.h."""
+    """``yapd_t3_layer`` of include/yapd_t3.h (``qbits`` 0: the bf16 weights; 4 or 8: ``q_*``)."""
     _fields_ = [("w_qkv", c_void), ("w_o", c_void), ("w_gate_up", c_void), ("w_down", c_void),
                 ("ln_in", c_void), ("ln_post", c_void), ("eps_in", c_float), ("eps_post", c_float),
-                ("kv_pool", c_void)]
+                ("kv_pool", c_void), ("qbits", c_int), ("q_qkv", T3QWeight), ("q_o", T3QWeight),
+                ("q_gate_up", T3QWeight), ("q_down", T3QWeight)]
 
 
 class T3Model(ctypes.Structure):
