@@ -265,7 +265,7 @@ def main():
 
     secondary = None
     if not args.no_secondary:
-        secondary = secondary_workloads(args, dev, model, eng, prefixes, lps)
+        secondary = secondary_workloads(args, dev, model, eng, prefixes, lps, sc_in)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -320,7 +320,7 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def secondary_workloads(args, dev, model, eng, prefixes, lps):
+def secondary_workloads(args, dev, model, eng, prefixes, lps, sc_in):
     """The other workloads' headline figures, measured in the same run after the step: the prefix
     prefill of the step's 512 rows (through the step's engine, rewriting the same KV), continuous
     batching on the same model, 30 layers of attention over the stress shape, and the vocoder's
@@ -341,6 +341,9 @@ def secondary_workloads(args, dev, model, eng, prefixes, lps):
     voc_args.no_cpu_baseline = True
     vc = vocoder_workload(voc_args, dev)
     torch.cuda.empty_cache()
+    qf = quant_figures(args, dev)
+    torch.cuda.empty_cache()
+    ms_q4 = quant_step(args, dev, model, prefixes, lps, sc_in, bits=4)
     return {
         "prefill": {"value": round(tokens / (ms_pf * 1e-3), 1), "unit": "prefix tokens/s", "ms": round(ms_pf, 3),
                     "wall_ms": round(wall_pf, 2), "prefix_tokens": tokens, "rows": len(lps), "layers": L,
@@ -355,6 +358,12 @@ def secondary_workloads(args, dev, model, eng, prefixes, lps):
                     "frac": vc["roofline"]["frac"], "shape": [vc["config"]["batch"], vc["config"]["channels"],
                                                               vc["config"]["samples"]],
                     "stitch_us": vc["kernels"]["stitch"]["us"], "stitch_jobs": vc["kernels"]["stitch"]["jobs"]},
+        "quant": {"projections": {f"bits{b}": {"ms_30_layers": round(ms, 4), "tflops": round(tf, 1),
+                                               "frac": round(tf / BF16_PEAK_TFLOPS, 4)} for b, (ms, tf) in qf.items()},
+                  "shapes": "qkv 3072x1024, o 1024x1024, gate/up 8192x1024, down 1024x4096 at M = 8192",
+                  "step_4bit": {"ms_per_step": round(ms_q4, 4),
+                                "value": round(args.pairs * args.block / (ms_q4 * 1e-3), 1),
+                                "unit": "speech tokens/s"}},
     }
 
 
@@ -675,10 +684,11 @@ def serve(args, dev, model=None):
         "commit_blocks": eng.commit_blocks, "wall_s": round(secs, 3)}
 
 
-def quant_projections(args, dev):
+def quant_figures(args, dev):
     """The four projections of 30 layers (qkv 3072x1024, o 1024x1024, gate/up
     8192x1024, down 1024x4096) as 4-bit and 8-bit affine-quantised GEMMs
-    (group 64, MLX layout, fp16 scales/biases) at M = 8192; weights N(0, 0.02)."""
+    (group 64, MLX layout, fp16 scales/biases) at M = 8192; weights N(0, 0.02).
+    Returns {bits: (ms for the 30 layers, TFLOP/s)}."""
     from yapd_amd.quant import qgemm_affine, quantize_affine
     M, L = 8192, args.layers
     shapes = [(3072, 1024), (1024, 1024), (8192, 1024), (1024, 4096)]
@@ -700,12 +710,17 @@ def quant_projections(args, dev):
         res[bits] = (ms, flops / (ms * 1e-3) / 1e12)
         log(f"quant {bits}-bit: {L} layers {ms:.3f} ms, {res[bits][1]:.0f} TF/s")
         del layers
+    return res
+
+
+def quant_projections(args, dev):
+    res = quant_figures(args, dev)
     ms4, tf4 = res[4]
     print(json.dumps({
         "metric": "affine-quantised projection TFLOP/s, 30 layers at M=8192", "value": round(tf4, 1),
         "unit": "TFLOP/s", "n_gpus": 1, "ms_per_step": round(ms4, 4), "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic (weights N(0,0.02) quantised; A N(0,1))",
-        "config": {"workload": "qkv/o/gate-up/down dequant GEMMs", "M": M, "layers": L, "group": 64,
+        "config": {"workload": "qkv/o/gate-up/down dequant GEMMs", "M": 8192, "layers": args.layers, "group": 64,
                    "bits": 4},
         "bits8": {"ms": round(res[8][0], 4), "tflops": round(res[8][1], 1),
                   "frac": round(res[8][1] / BF16_PEAK_TFLOPS, 4)},
@@ -713,13 +728,45 @@ def quant_projections(args, dev):
                      "frac": round(tf4 / BF16_PEAK_TFLOPS, 4)}}), flush=True)
 
 
+def quant_step(args, dev, model, prefixes, lps, sc_in, bits=4):
+    """The benched step on ``bits``-bit weights: a quantised engine on the same model, prefixes and
+    block (every layer projection affine-quantised, engines/mlx.py:221-255).  Returns ms per step."""
+    from yapd_amd.engines.hip import HipEngine
+    from yapd_amd.step import DecodeStep
+    from yapd_amd.synthetic import MASK_ID, STOP_ID
+    Bp, bl = args.pairs, args.block
+    eng = HipEngine(model, max(lps) + 2 * bl, torch.bfloat16, batch_size=2 * Bp, page_table_seed=args.seed + 2,
+                    quant_bits=bits)
+    sos = eng.prefix_forward([p.to(dev) for p in prefixes + prefixes])
+    step = DecodeStep(eng, model, n_pairs=Bp, block_size=bl, log_prior=sc_in.log_prior.to(dev), mask_id=MASK_ID,
+                      stop_id=STOP_ID, num_steps=10, time_shift_tau=3.0, omnivoice_t_shift=0.5, cfg_scale=0.5)
+    step.xt.copy_(sc_in.xt.to(dev))
+    step.k_step.copy_(sc_in.k_step.to(dev))
+    step.capture(lps, sos)
+    for _ in range(3):
+        step.replay()
+    torch.cuda.synchronize(dev)
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(10):
+        step.replay()
+    en.record()
+    torch.cuda.synchronize(dev)
+    ms = st.elapsed_time(en) / 10
+    log(f"{bits}-bit step {ms:.3f} ms")
+    del step, eng
+    torch.cuda.empty_cache()
+    return ms
+
+
 def kernel_sample(dev, Bp, bl):
     """Every kernel of the step at the bench shape, three dispatches each and in this order, for
     rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE / MFMA counters per dispatch): gate/up + SiLU, QKV +
     RoPE + KV write, o_proj + residual, down_proj + residual, RMSNorm, speech head (two launches
     per call), paged attention over three layers' pools (each ~0.9 GB of K/V, so no dispatch finds
-    its pool in the 256 MB MALL), scoring on two alternating 268 MB logits sets, then a plain
-    1 GiB device copy (the counter calibration)."""
+    its pool in the 256 MB MALL), scoring on two alternating 268 MB logits sets, the 4-bit
+    quantised gate/up and down projections at M = 8192, then a plain 1 GiB device copy (the
+    counter calibration)."""
     from yapd_amd import kernels
     from yapd_amd.engines.hip import HipEngine
     from yapd_amd.paged import AttnPlan
@@ -772,6 +819,14 @@ def kernel_sample(dev, Bp, bl):
                                                          logits_buf[..., :V]))
     run("attention", lambda i: plan.run(q, eng.kv.pools[i], eng.kv.table, out, 0.125))
     run("scoring", lambda i: scorer(sets[i % 2][..., :V], xt, k_step, layout="stacked"))
+    # the quantised projections at C5's M = 8192: 4-bit gate/up (N 8192, K 1024) and down (N 1024, K 4096)
+    from yapd_amd.quant import qgemm_affine, quantize_affine
+    q_gu, q_d = quantize_affine(w["wgu"], 4), quantize_affine(w["wd"], 4)
+    out_gu = torch.empty(8192, 2 * F, dtype=torch.bfloat16, device=dev)
+    out_d = torch.empty(8192, D, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize(dev)
+    run("qgemm4_gate_up", lambda i: qgemm_affine(normed[:8192], *q_gu, 4, out=out_gu))
+    run("qgemm4_down", lambda i: qgemm_affine(act[:8192], *q_d, 4, out=out_d))
     run("copy_1GiB", lambda i: dst.copy_(src))
     torch.cuda.synchronize(dev)
     kv_len = plan.kv_len_host

@@ -111,13 +111,13 @@ def test_quantised_engine_equals_bf16_engine_on_dequantised_weights(dev, bits, p
 def test_thirty_layer_step_on_4bit_weights_against_the_oracle(dev):
     layers = 30
     lens = uniform_lengths(PAIRS, 150, 600, seed=71)
-    model_q = make_t3(n_layers=layers, seed=70, device=dev)
+    model_q = make_t3(n_layers=layers, seed=70, norm_jitter=True, learned_pos_emb=True, device=dev)
     w = build(dev, model_q, lens, 4, seed=72)
     hid, logits, _, res = replay(w)
     assert torch.isfinite(hid.float()).all()
     decisions_vs_oracle(res, logits, w)
     # the reference model: the same weights, dequantised
-    model_e = make_t3(n_layers=layers, seed=70, device=dev)
+    model_e = make_t3(n_layers=layers, seed=70, norm_jitter=True, learned_pos_emb=True, device=dev)
     dequantize_model_(model_e, 4)
     eng = w["eng"]
     p = min(range(PAIRS), key=lambda i: lens[i])
