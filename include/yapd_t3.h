@@ -128,7 +128,10 @@ int yapd_attn_paged_block(const void* q, const void* kv_pool, int64_t n_pages, c
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops).  Every call on one GPU shares that GPU's
  * array, so calls that overlap on one GPU race (use one stream per GPU or
- * order the streams).  Results equal yapd_attn_paged_block's bit for bit. */
+ * order the streams).  The first call on a GPU that splits a row looks up
+ * the array's device address (hipGetSymbolAddress, not a stream operation);
+ * if `stream` is being captured then, the lookup runs in relaxed capture mode
+ * for the calling thread.  Results equal yapd_attn_paged_block's bit for bit. */
 int yapd_attn_paged_block_noalloc(const void* q, const void* kv_pool, int64_t n_pages, const int32_t* page_table,
                                   int table_stride, int table_cols, const int32_t* kv_len, int rows, int bl,
                                   int n_heads, const int32_t* work, int n_work, const int32_t* merge, int n_merge,

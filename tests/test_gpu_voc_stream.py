@@ -156,8 +156,14 @@ def test_worker_streams_equal_the_oracle(dev, cfg):
         assert len(ref) == len(toks) * 960 - dropped
 
 
-def test_worker_lanes_on_threads(dev):
-    cfg = dict(chunk_first=12, chunk=40, lookback=16)
+# with a second-chunk size or top-up widths, a request's top-up chunk runs on the first-chunk lane
+# while its next chunk can go to the bulk lane, which then blends with a tail the other lane's
+# stream wrote (ordered by the event stored with the tail)
+@pytest.mark.parametrize("cfg", [dict(chunk_first=12, chunk=40, lookback=16),
+                                 dict(chunk_first=12, chunk=80, lookback=16, chunk_second=20),
+                                 dict(chunk_first=12, chunk=40, lookback=8, topup_sizes=(8, 16, 24))],
+                         ids=["default", "chunk_second", "topup"])
+def test_worker_lanes_on_threads(dev, cfg):
     s3 = TableS3Gen(vocab=512, seed=7, device=dev)
     voc = Vocoder(s3, TableS3Gen.ref_dict(), dev, max_batch=16, first_max_batch=8, **cfg)
     worker = threading.Thread(target=voc.run, daemon=True)

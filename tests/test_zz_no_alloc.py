@@ -3,6 +3,10 @@ array) against ``yapd_attn_paged_block`` (caller-provided workspace), both
 called through the C ABI: bit-identical outputs on two calls in a row, the
 second smaller, plus an unsplit call and the size limit."""
 
+import os
+import subprocess
+import sys
+
 import pytest
 import torch
 
@@ -65,3 +69,46 @@ def test_noalloc_rejects_partials_beyond_the_static_array(dev):
                       kernels.stream_ptr(dev))
     assert rc == 1
     assert "static scratch holds" in kernels.load_library().yapd_last_error().decode()
+
+
+def test_noalloc_under_graph_capture_equals_eager(dev):
+    """The entry point captured in a HIP graph (torch.cuda.CUDAGraph) and replayed three times, with
+    eager calls of the workspace entry point between the replays, equals the eager call bit for bit
+    (the static array's address was looked up by an earlier call on this device)."""
+    rows, bl = 4, 32
+    q, pool, table, kv_len, Ks, Vs = build_case(rows, bl, [1500, 33, 700, 2000], seed=34)
+    q, pool, tab = q.to(dev), pool.to(dev), torch.from_numpy(table).to(dev)
+    plan = AttnPlan(kv_len, bl, q.shape[2], dev, target_items=64, min_split_keys=32)
+    assert plan.n_slots > 0
+    eager = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
+    plan.run(q, pool, tab, eager, 0.125)
+    out = torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    n_merge = int(plan.merge.shape[0])
+
+    def call():
+        kernels.check(noalloc_fn()(q.data_ptr(), pool.data_ptr(), pool.shape[0], tab.data_ptr(), tab.stride(0),
+                                   tab.shape[1], plan.kv_len.data_ptr(), rows, bl, q.shape[2],
+                                   plan.work.data_ptr(), int(plan.work.shape[0]), plan.merge.data_ptr(), n_merge,
+                                   None, int(plan.n_slots), 0.125, 0, out.data_ptr(), kernels.stream_ptr(dev)))
+    call()  # eager, outside the capture
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        scratch_other = torch.empty_like(eager)
+        plan.run(q, pool, tab, scratch_other, 0.125)  # eager work between the replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process(dev):
+    """In a new process, the first call of the entry point runs inside a graph capture, so the
+    scratch address is looked up during the capture (in relaxed capture mode); the replays must
+    equal the eager workspace entry point (tests/_noalloc_capture_child.py)."""
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_noalloc_capture_child.py")
+    res = subprocess.run([sys.executable, child], capture_output=True, text=True, timeout=180)
+    assert res.returncode == 0 and "OK" in res.stdout, res.stdout[-2000:] + res.stderr[-2000:]

@@ -26,15 +26,33 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_for_current_device(float** out) {
+// The lookup is not a stream operation.  When the first call on a device comes
+// while `stream` is being captured into a graph, it runs with this thread's
+// capture mode switched to relaxed (the documented way for a library to make
+// such a call during a capture) and the mode is restored afterwards.
+int scratch_for_current_device(float** out, hipStream_t stream) {
   int dev = -1;
   int rc = check_hip(hipGetDevice(&dev), "attn_noalloc: hipGetDevice");
   if (rc != YAPD_OK) return rc;
   YAPD_REQUIRE(dev >= 0 && dev < kMaxDevices, "attn_noalloc: device %d outside [0, %d)", dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    rc = check_hip(hipStreamIsCapturing(stream, &cap), "attn_noalloc: hipStreamIsCapturing");
+    if (rc != YAPD_OK) return rc;
+    const bool capturing = cap == hipStreamCaptureStatusActive;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (capturing) {
+      rc = check_hip(hipThreadExchangeStreamCaptureMode(&mode), "attn_noalloc: hipThreadExchangeStreamCaptureMode");
+      if (rc != YAPD_OK) return rc;
+    }
     void* p = nullptr;
-    rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "attn_noalloc: hipGetSymbolAddress(scratch)");
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (capturing) {
+      rc = check_hip(hipThreadExchangeStreamCaptureMode(&mode), "attn_noalloc: restoring the capture mode");
+      if (rc != YAPD_OK) return rc;
+    }
+    rc = check_hip(e, "attn_noalloc: hipGetSymbolAddress(scratch)");
     if (rc != YAPD_OK) return rc;
     YAPD_REQUIRE(p != nullptr && (reinterpret_cast<uintptr_t>(p) & 255u) == 0,
                  "attn_noalloc: scratch address is not 256-byte aligned");
@@ -68,7 +86,7 @@ extern "C" int yapd_attn_paged_block_noalloc(const void* q, const void* kv_pool,
                  "the static scratch holds %lld",
                  static_cast<long long>(need), n_slots, bl, n_heads, static_cast<long long>(yapd::kScratchBytes));
     float* base = nullptr;
-    rc = yapd::scratch_for_current_device(&base);
+    rc = yapd::scratch_for_current_device(&base, static_cast<hipStream_t>(stream));
     if (rc != YAPD_OK) return rc;
     part_o = base;
     part_ml = base + o_floats;  // o_floats is a multiple of 64 floats: 16-byte aligned

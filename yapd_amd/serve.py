@@ -64,6 +64,7 @@ class Request:
     sink: object = None
     emitted_tok: int = 0      # committed tokens handed to the vocoder
     voc_tail: object = None   # crossfade tail of the last chunk (device tensor)
+    voc_tail_ready: object = None  # event recorded after the launch that wrote voc_tail
     first_chunk_sent: bool = False
     finished: bool = False    # audio stream closed
     t_first_pcm: float = 0.0

@@ -343,6 +343,11 @@ class Vocoder:
                 n_blend, tail_in = 0, -1
                 tail = None if j.first else j.req.voc_tail
                 if tail is not None and off - lo > 0:
+                    ready = getattr(j.req, "voc_tail_ready", None)
+                    if ready is not None and torch.is_tensor(tail) and tail.is_cuda:
+                        # the tail may come from another lane's stream: order this
+                        # stream after the launch that wrote it
+                        stream.wait_event(ready)
                     if not torch.is_tensor(tail):  # handed over from another process as numpy
                         tail = torch.from_numpy(np.ascontiguousarray(tail, dtype=np.float32).reshape(-1))
                     n_blend = min(tail.numel(), off - lo, n_seg)
@@ -363,9 +368,12 @@ class Vocoder:
             t_out = torch.empty(n_tail_out, fade, dtype=torch.float32, device=dev) if n_tail_out else None
             kernels.voc_stitch(wavs, torch.tensor(rows, dtype=torch.int32).to(dev), self.fade_in, self.fade_out,
                                self.trim, t_in, t_out, pcm)
-            for r in rows:  # the next launch (or the next batch) blends with these tails
+            written = torch.cuda.Event()
+            written.record(stream)
+            for r in rows:  # the next launch (or the next batch, on any lane) blends with these tails
                 tails_after[r[0]] = t_out[r[8]] if r[8] >= 0 else None
                 real[r[0]].req.voc_tail = tails_after[r[0]]
+                real[r[0]].req.voc_tail_ready = written
         pcm_host = torch.empty(pcm.numel(), dtype=torch.int16, pin_memory=True)
         pcm_host.copy_(pcm, non_blocking=True)
         done = torch.cuda.Event()
