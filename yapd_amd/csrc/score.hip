@@ -3,16 +3,19 @@
 // One workgroup of 16 waves per CFG pair.  Each wave scores whole positions:
 // it streams the position's cond and null logit rows once from HBM (dword
 // loads; rows are only 4-byte aligned since V = 8194), each lane keeping a
-// running (max, sum-exp) per branch and the argmax of the guided score, then
-// reduces across the wave on DPP.  The guided argmax uses (1+w)*lc - w*lu,
-// which differs from the reference's lsc + w*(lsc - lsu)
-// (server/engine.py:536-539) only by a per-row constant.  The pair's keys go
-// to LDS and one wave runs the per-pair decision rule of
-// server/engine.py:563-593: ranks by pairwise comparison, the linear quantile
-// with the reference's fp32 op order, top-n unmask.  Keeping the pair in one
-// workgroup makes the handoff an LDS barrier: across workgroups it would need
-// agent-scope release/acquire fences, which on a multi-XCD part write back /
-// invalidate the XCD's L2, or a second launch.
+// running (max, sum-exp) per branch and its best guided score, then reduces
+// across the wave on DPP.  The guided argmax uses (1+w)*lc - w*lu, which
+// differs from the reference's lsc + w*(lsc - lsu) (server/engine.py:536-539)
+// only by a per-row constant; the index of the maximum is found once per
+// position from LDS copies of the passes that raised a lane's best.  The
+// position's statistics go to LDS, and after one barrier wave 0 finishes the
+// pair lane-parallel (lane = position): the pmi of each sampled token, then
+// the decision rule of server/engine.py:563-593 -- ranks by pairwise
+// comparison, the linear quantile with the reference's fp32 op order, top-n
+// unmask.  Keeping the pair in one workgroup makes the handoff an LDS barrier:
+// across workgroups it would need agent-scope release/acquire fences, which
+// on a multi-XCD part write back / invalidate the XCD's L2, or a second
+// launch.
 #include <cmath>
 
 #include "common.h"
@@ -86,25 +89,15 @@ __device__ __forceinline__ RowStats merge_stats(RowStats a, RowStats b) {
   return {m, sa + sb};
 }
 
-struct Best {
-  float g;
-  int idx;
-  float lc, lu;
-};
-
-__device__ __forceinline__ bool better(const Best& o, const Best& cur) {
-  return o.g > cur.g || (o.g == cur.g && o.idx < cur.idx);
-}
-
-
 __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
 // Wave reductions on DPP: within each 16-lane row the two quad permutes, the
 // half-row mirror and the row mirror leave the row's result in all of its
-// lanes; the four row results are then combined from SGPRs (readlane), so
-// every lane ends with the wave's result and no LDS permute is issued.
+// lanes; v_permlane16_swap and v_permlane32_swap then combine the four row
+// results, so every lane ends with the wave's result and no LDS permute is
+// issued.
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
@@ -121,47 +114,49 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
   v = op(v, dpp_f<kDppQuadXor2>(v));
   v = op(v, dpp_f<kDppHalfMirror>(v));
   v = op(v, dpp_f<kDppMirror>(v));
-  return op(op(readlane_f(v, 0), readlane_f(v, 16)), op(readlane_f(v, 32), readlane_f(v, 48)));
+  // rows: v_permlane16_swap pairs row 0 with 1 and 2 with 3, v_permlane32_swap
+  // the halves -- op(op(r0, r1), op(r2, r3)) in every lane
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
 }
 
-// The argmax (value, lowest index) of a wave, in every lane.
-__device__ __forceinline__ Best wave_best(Best b) {
-  {
-    const Best o{dpp_f<kDppQuadXor1>(b.g), dpp_i<kDppQuadXor1>(b.idx), 0.f, 0.f};
-    if (better(o, b)) b = o;
-  }
-  {
-    const Best o{dpp_f<kDppQuadXor2>(b.g), dpp_i<kDppQuadXor2>(b.idx), 0.f, 0.f};
-    if (better(o, b)) b = o;
-  }
-  {
-    const Best o{dpp_f<kDppHalfMirror>(b.g), dpp_i<kDppHalfMirror>(b.idx), 0.f, 0.f};
-    if (better(o, b)) b = o;
-  }
-  {
-    const Best o{dpp_f<kDppMirror>(b.g), dpp_i<kDppMirror>(b.idx), 0.f, 0.f};
-    if (better(o, b)) b = o;
-  }
-  Best r{readlane_f(b.g, 0), __builtin_amdgcn_readlane(b.idx, 0), 0.f, 0.f};
-#pragma unroll
-  for (int q = 16; q < 64; q += 16) {
-    const Best o{readlane_f(b.g, q), __builtin_amdgcn_readlane(b.idx, q), 0.f, 0.f};
-    if (better(o, r)) r = o;
-  }
-  return r;
+// The minimum of a wave, in every lane.
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, dpp_i<kDppQuadXor1>(v));
+  v = min(v, dpp_i<kDppQuadXor2>(v));
+  v = min(v, dpp_i<kDppHalfMirror>(v));
+  v = min(v, dpp_i<kDppMirror>(v));
+  const auto s16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = min(static_cast<int>(s16[0]), static_cast<int>(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return min(static_cast<int>(s32[0]), static_cast<int>(s32[1]));
 }
+
+typedef __attribute__((ext_vector_type(2))) uint64_t u64x2_t;
+
+// A scored position: the sampled token and each branch's maximum and sum of
+// exponentials, the same in every lane.
+struct ItemStats {
+  int x;
+  float Mc, Sc, Mu, Su;
+};
 
 // One (pair, position) scored by one wave: a streaming pass over the cond
 // and null rows (dword loads; rows are only 4-byte aligned at V = 8194), each
-// lane keeping running softmax statistics and its argmax, then wave
-// reductions on DPP.  Per element the VALU work is what the math needs (bf16
-// unpack, max, one FMA + v_exp and an add per branch, the guided score and a
-// compare/select for the argmax).  A pass's 32 loads per lane are issued back
-// to back; the other waves of the workgroup (4 per SIMD) cover their latency.
-// Returns the token (every lane) and the pmi (lane 0).
+// lane keeping running softmax statistics and its best guided score, then
+// wave reductions on DPP.  Per element the VALU work is what the math needs
+// (bf16 unpack, max, one FMA + v_exp and an add per branch, the guided score
+// and its maximum).  A pass's 32 loads per lane are issued back to back; the
+// other waves of the workgroup (4 per SIMD) cover their latency.  The argmax
+// index is not searched per pass: a pass that raises a lane's best stores its
+// guided values to the lane's part of the wave's LDS slot (``sav``, 8 KB),
+// and once per position the lowest index at the wave's maximum is read back
+// from the slots of the lanes that hold it.
 template <bool kHasU, bool kSample, bool kRank>
-__device__ __forceinline__ void score_item(const ScoreParams& P, int item, int pair, int pos, int lane, int& x_out,
-                                           float& pmi_out) {
+__device__ __forceinline__ ItemStats score_item(const ScoreParams& P, int item, int pair, int pos, int lane,
+                                                float4* __restrict__ sav) {
   const int64_t crow = static_cast<int64_t>(P.cond_row0) + static_cast<int64_t>(pair) * P.pair_row_step;
   const uint16_t* rc = P.logits + crow * P.seq_stride + static_cast<int64_t>(pos) * P.pos_stride;
   const uint16_t* ru = rc + static_cast<int64_t>(P.null_row_offset) * P.seq_stride;
@@ -177,7 +172,8 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
 
   RowStats sc{-INFINITY, 0.f}, su{-INFINITY, 0.f};
   float best_g = -INFINITY;
-  int best_v = 0x7fffffff;
+  int best_v = 0x7fffffff;  // the lane's best element when it came from the tail
+  int best_pass = -1;       // else the pass whose guided values sit in the lane's slot
 
   // Guided score of element v (+ T * Gumbel noise when sampling).  Without
   // sampling only its order matters, and for w > 0 the argmax ranks by
@@ -219,6 +215,14 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
       if (kHasU) xu[u] = wu[base + u * 64 + lane];
     }
   };
+  // the first tail word, requested with the first pass rather than after the
+  // last one
+  const int jt = n_pass * kPass + lane;
+  uint32_t tc0 = 0u, tu0 = 0u;
+  if (jt < nw) {
+    tc0 = wc[jt];
+    if (kHasU) tu0 = wu[jt];
+  }
   for (int pi = 0; pi < n_pass; ++pi) {
     const int base = pi * kPass;
     load_pass(base);
@@ -251,17 +255,17 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
 #pragma unroll
     for (int e = 1; e < 2 * kUnroll; ++e) pg = fmaxf(pg, gv[e]);
     if (pg > best_g) {
-      int pe = 0;
-#pragma unroll
-      for (int e = 2 * kUnroll - 1; e >= 0; --e) pe = gv[e] == pg ? e : pe;
       best_g = pg;
-      best_v = 2 * (base + (pe >> 1) * 64 + lane) + (pe & 1);
+      best_pass = pi;
+#pragma unroll
+      for (int q = 0; q < kUnroll / 2; ++q)
+        sav[q * 64 + lane] = make_float4(gv[4 * q], gv[4 * q + 1], gv[4 * q + 2], gv[4 * q + 3]);
     }
   }
   // Tail: the remaining dwords, one per lane at a time.
-  for (int j = n_pass * kPass + lane; j < nw; j += 64) {
-    const uint32_t tc = wc[j];
-    const uint32_t tu = kHasU ? wu[j] : 0u;
+  for (int j = jt; j < nw; j += 64) {
+    const uint32_t tc = j == jt ? tc0 : wc[j];
+    const uint32_t tu = j == jt ? tu0 : kHasU ? wu[j] : 0u;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const float lc = h ? bf16hi(tc) : bf16lo(tc);
@@ -272,6 +276,7 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
       if (g > best_g) {
         best_g = g;
         best_v = 2 * j + h;
+        best_pass = -1;
       }
     }
   }
@@ -284,6 +289,7 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
     if (g > best_g) {
       best_g = g;
       best_v = V - 1;
+      best_pass = -1;
     }
   }
 
@@ -293,35 +299,68 @@ __device__ __forceinline__ void score_item(const ScoreParams& P, int item, int p
   auto add_op = [](float a, float b) { return a + b; };
   const float Mc = wave_reduce(sc.m, fmax_op);
   const float Mu = kHasU ? wave_reduce(su.m, fmax_op) : 0.f;
-  const Best best = wave_best(Best{best_g, best_v, 0.f, 0.f});
+  // argmax: the lowest element index whose guided value is the wave's maximum,
+  // as torch.argmax.  Each lane's best is its first occurrence in index order
+  // (strict > above); a lane whose best lies in a pass finds it in its slot:
+  // lane e < 2 * kUnroll checks element e of that pass.  One lane holds the
+  // maximum unless values tie exactly.
+  const float Gm = wave_reduce(best_g, fmax_op);
+  // the slots were written by other lanes of this wave: LDS runs a wave's
+  // accesses in order, the fences keep the compiler from moving them
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int best_idx = best_g == Gm && best_pass < 0 ? best_v : 0x7fffffff;
+  uint64_t cand = __ballot(best_g == Gm && best_pass >= 0);
+  const float* savf = reinterpret_cast<const float*>(sav);
+  while (cand) {
+    const int L = __ffsll(static_cast<unsigned long long>(cand)) - 1;
+    cand &= cand - 1;
+    const int pL = __builtin_amdgcn_readlane(best_pass, L);
+    if (lane < 2 * kUnroll && savf[((lane >> 2) * 64 + L) * 4 + (lane & 3)] == Gm)
+      best_idx = min(best_idx, 2 * (pL * kPass + (lane >> 1) * 64 + L) + (lane & 1));
+  }
+  best_idx = wave_min_i(best_idx);
+  // the next position's slot writes stay after these reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // a lane with no finite value (m = -inf) contributes nothing; so does a row
   // whose maximum is -inf, whose sum stays 0
   const float Sc = wave_reduce(sc.m == -INFINITY ? 0.f : sc.s * __builtin_amdgcn_exp2f((sc.m - Mc) * kLog2e), add_op);
   const float Su = kHasU ? wave_reduce(su.m == -INFINITY ? 0.f : su.s * __builtin_amdgcn_exp2f((su.m - Mu) * kLog2e),
                                        add_op)
                          : 0.f;
-  const int x = best.idx < V ? best.idx : 0;  // a row of only -inf / NaN scores: token 0, as torch.argmax
-  x_out = x;
-  pmi_out = 0.f;
-  if (lane == 0) {
-    const float lpr = P.log_prior[x];
-    // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
-    const float lcx = bf16_to_f32(rc[x]);
-    float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lcx - Mc), Sc), 1e-8f)), lpr);
-    if (kHasU) {
-      const float lux = bf16_to_f32(ru[x]);
-      const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lux - Mu), Su), 1e-8f)), lpr);
-      pmi = __fsub_rn(__fmul_rn(w1, pmi), __fmul_rn(w, pmi_u));
-    }
-    if (P.pos_gumbel) {
-      const int64_t xt = P.xt_in[item];
-      if (xt == P.mask_id) {
-        const u32x4_t r = philox4x32_10(0xffffffffu, static_cast<uint32_t>(item), off0, off1, key0, key1);
-        pmi = __fadd_rn(pmi, gumbel_from_u32(r.x));
-      }
-    }
-    pmi_out = pmi;
+  const int x = best_idx < V ? best_idx : 0;  // a row of only -inf / NaN scores: token 0, as torch.argmax
+  return ItemStats{x, Mc, Sc, Mu, Su};
+}
+
+// The pmi of one scored item from its row statistics (lane-parallel: one
+// item per lane).
+template <bool kHasU>
+__device__ __forceinline__ float item_pmi(const ScoreParams& P, int item, int pair, int pos, const ItemStats& st,
+                                          int64_t xt) {
+  const int64_t crow = static_cast<int64_t>(P.cond_row0) + static_cast<int64_t>(pair) * P.pair_row_step;
+  const uint16_t* rc = P.logits + crow * P.seq_stride + static_cast<int64_t>(pos) * P.pos_stride;
+  const uint16_t* ru = rc + static_cast<int64_t>(P.null_row_offset) * P.seq_stride;
+  const int x = st.x;
+  const float w = P.cfg_w, w1 = P.cfg_w1;
+  const float lpr = P.log_prior[x];
+  // probs.gather(sampled).clamp_min(1e-8).log() - log_prior[sampled]
+  const float lcx = bf16_to_f32(rc[x]);
+  float pmi = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lcx - st.Mc), st.Sc), 1e-8f)), lpr);
+  if (kHasU) {
+    const float lux = bf16_to_f32(ru[x]);
+    const float pmi_u = __fsub_rn(logf(fmaxf(__fdiv_rn(expf(lux - st.Mu), st.Su), 1e-8f)), lpr);
+    pmi = __fsub_rn(__fmul_rn(w1, pmi), __fmul_rn(w, pmi_u));
   }
+  if (P.pos_gumbel && xt == P.mask_id) {
+    const uint32_t key0 = static_cast<uint32_t>(P.seed), key1 = static_cast<uint32_t>(P.seed >> 32);
+    const uint32_t off0 = static_cast<uint32_t>(P.rng_offset), off1 = static_cast<uint32_t>(P.rng_offset >> 32);
+    const u32x4_t r = philox4x32_10(0xffffffffu, static_cast<uint32_t>(item), off0, off1, key0, key1);
+    pmi = __fadd_rn(pmi, gumbel_from_u32(r.x));
+  }
+  return pmi;
 }
 
 // The per-pair inputs of the decision rule, one entry per lane: every load is
@@ -350,7 +389,7 @@ __device__ __forceinline__ PairInputs load_pair_inputs(const ScoreParams& P, int
 // q_k (m-1), linear quantile, n = min(max(min(sched, m), n_quant), m), top-n
 // unmask, n_mask_after and hit_eos.
 __device__ __forceinline__ void decide_pair(const ScoreParams& P, int pair, int lane, const PairInputs& in, float key,
-                                            int64_t smp) {
+                                            int64_t smp, uint64_t* s_ka, uint64_t* s_kd) {
   const int bl = P.bl;
   const int64_t ib = static_cast<int64_t>(pair) * bl;
   const bool valid = lane < bl;
@@ -360,14 +399,55 @@ __device__ __forceinline__ void decide_pair(const ScoreParams& P, int pair, int 
   const uint64_t bal = __ballot(msk);
   const int m = __popcll(bal);
 
+  // Ranks among the masked positions.  asc counts masked j with p_j < key, or
+  // p_j == key and j < lane; desc the same with p_j > key.  Each position's
+  // key becomes two 64-bit words -- its float order as an unsigned number
+  // (-0 taken as +0), or that number's complement, above the position index
+  // -- so one unsigned compare decides both the order and the tie.  Positions
+  // that are not masked and NaN keys hold all ones, which no compare counts, as
+  // no float compare counts a NaN.  With at most 32 positions the two halves
+  // of the wave each compare with half of the keys.
+  const bool num = msk && key == key;
+  const uint32_t ku = __float_as_uint(key + 0.f);
+  const uint32_t ord = ku ^ (static_cast<uint32_t>(static_cast<int32_t>(ku) >> 31) | 0x80000000u);
+  s_ka[lane] = num ? (static_cast<uint64_t>(ord) << 32 | static_cast<uint32_t>(lane)) : ~0ull;
+  s_kd[lane] = num ? (static_cast<uint64_t>(~ord) << 32 | static_cast<uint32_t>(lane)) : ~0ull;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool split = bl <= 32;
+  const int own = split ? (lane & 31) : lane;
+  const int j0 = split ? (lane >> 5) * 16 : 0;
+  const int nj = split ? 16 : bl;  // entries past bl hold all ones
+  const uint64_t a_own = s_ka[own], d_own = s_kd[own];
   int asc = 0, desc = 0;
-  for (int j = 0; j < bl; ++j) {
-    if ((bal >> j) & 1ull) {
-      const float pj = readlane_f(key, j);
-      asc += (pj < key) || (pj == key && j < lane);
-      desc += (pj > key) || (pj == key && j < lane);
+  if (split) {  // all 16 words of the half requested at once: one LDS round trip
+    u64x2_t a2[8], d2[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      a2[t] = *reinterpret_cast<const u64x2_t*>(s_ka + j0 + 2 * t);
+      d2[t] = *reinterpret_cast<const u64x2_t*>(s_kd + j0 + 2 * t);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      asc += (a2[t][0] < a_own) + (a2[t][1] < a_own);
+      desc += (d2[t][0] < d_own) + (d2[t][1] < d_own);
+    }
+  } else {
+    for (int t = 0; t < nj; t += 2) {
+      const u64x2_t a2 = *reinterpret_cast<const u64x2_t*>(s_ka + j0 + t);
+      const u64x2_t d2 = *reinterpret_cast<const u64x2_t*>(s_kd + j0 + t);
+      asc += (a2[0] < a_own) + (a2[1] < a_own);
+      desc += (d2[0] < d_own) + (d2[1] < d_own);
     }
   }
+  if (split) {
+    const auto sa = __builtin_amdgcn_permlane32_swap(asc, asc, false, false);
+    const auto sd = __builtin_amdgcn_permlane32_swap(desc, desc, false, false);
+    asc = static_cast<int>(sa[0]) + static_cast<int>(sa[1]);
+    desc = static_cast<int>(sd[0]) + static_cast<int>(sd[1]);
+  }
+  if (!num) asc = desc = 0;  // a NaN key compares false with every key
   int kc = k < P.K - 1 ? static_cast<int>(k) : P.K - 1;
   kc = kc < 0 ? 0 : kc;
   // p = q_t[k] * (m-1).clamp_min(0).float(); lo/hi = floor/ceil; linear interpolation.
@@ -400,33 +480,40 @@ __device__ __forceinline__ void decide_pair(const ScoreParams& P, int pair, int 
   }
 }
 
-// One workgroup per pair: wave w scores positions w, w + kPairWaves, ..., and
-// wave 0 then applies the decision rule to the pair's keys from LDS -- one
-// launch, no handoff through global memory between workgroups.
+// One workgroup per pair: wave w scores positions w, w + kPairWaves, ...
+// into LDS; after the barrier wave 0 computes the pair's pmi lane-parallel --
+// the gathers of log_prior and the logits at the sampled tokens are one round
+// trip for the whole pair, and the per-pair inputs ride along -- and applies
+// the decision rule.  One launch, no handoff through global memory between
+// workgroups.
 template <bool kHasU, bool kSample, bool kRank = false>
 __global__ __launch_bounds__(64 * kPairWaves) void score_pair_kernel(const ScoreParams P) {
   const int pair = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __shared__ float s_key[64];
-  __shared__ int64_t s_smp[64];
-  PairInputs in{};
-  if (wave == 0) in = load_pair_inputs(P, pair, lane);  // in flight while wave 0 scores
+  __shared__ ItemStats s_st[64];
+  __shared__ __align__(16) uint64_t s_ka[64];
+  __shared__ __align__(16) uint64_t s_kd[64];
+  __shared__ float4 s_sav[kPairWaves * (kUnroll / 2) * 64];  // 8 KB per wave: guided values of a lane's best pass
   for (int pos = wave; pos < P.bl; pos += kPairWaves) {
-    const int item = pair * P.bl + pos;
-    int x;
-    float pmi;
-    score_item<kHasU, kSample, kRank>(P, item, pair, pos, lane, x, pmi);
-    if (lane == 0) {
-      P.sampled[item] = x;
-      P.pmi[item] = pmi;
-      s_key[pos] = pmi;
-      s_smp[pos] = x;
-    }
+    const ItemStats st = score_item<kHasU, kSample, kRank>(P, pair * P.bl + pos, pair, pos, lane,
+                                                           s_sav + wave * (kUnroll / 2) * 64);
+    if (lane == 0) s_st[pos] = st;
   }
   __syncthreads();
   if (wave == 0) {
+    const PairInputs in = load_pair_inputs(P, pair, lane);
     const bool valid = lane < P.bl;
-    decide_pair(P, pair, lane, in, valid ? s_key[lane] : 0.f, valid ? s_smp[lane] : 0);
+    float pmi = 0.f;
+    int64_t x = 0;
+    if (valid) {
+      const int item = pair * P.bl + lane;
+      const ItemStats st = s_st[lane];
+      pmi = item_pmi<kHasU>(P, item, pair, lane, st, in.xt);
+      x = st.x;
+      P.sampled[item] = x;
+      P.pmi[item] = pmi;
+    }
+    decide_pair(P, pair, lane, in, pmi, x, s_ka, s_kd);
   }
 }
 
