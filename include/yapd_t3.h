@@ -32,7 +32,8 @@ extern "C" {
 /* Message for the last nonzero return on this thread ("" if none). */
 const char* yapd_last_error(void);
 
-/* ABI revision of this library (bumped on any signature change). */
+/* ABI revision of this library (bumped on any signature or struct layout
+ * change; 3 added the quantised-weight fields of yapd_t3_layer). */
 int yapd_abi_version(void);
 
 /* ------------------------------------------------------------------------ *
@@ -61,7 +62,7 @@ int yapd_abi_version(void);
  * Outputs [n_pairs, bl]: sampled (int64), pmi (fp32), unmask (u8), xt_out
  * (int64); per pair: n_mask_after (int32), hit_eos (u8).  1 <= bl <= 64, 1 <= K <= 64.
  * One launch: a workgroup per pair, one wave per position, then the pair's
- * decision by one wave from LDS.
+ * pmi and decision by one wave (lane = position) from LDS.
  * ------------------------------------------------------------------------ */
 
 int yapd_score_cfg_pmi_unmask(
@@ -169,9 +170,10 @@ int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, 
  * (engines/flashinfer.py:992-1035: input_layernorm, then the projections, RoPE
  * and the pool write): x [M, K] contiguous bf16 rows are normalised into the
  * caller's workspace normed [M, K] (HF LlamaRMSNorm, as yapd_rmsnorm with x),
- * then yapd_gemm_qkv_rope_kv runs on normed.  Two launches on `stream`; every
- * argument of both is checked before the first (a rejected call launches
- * nothing). */
+ * then yapd_gemm_qkv_rope_kv runs on normed.  A composition, not a fused
+ * kernel: two launches on `stream` (the norm is a separate row pass, as in the
+ * step driver), every argument of both checked before the first (a rejected
+ * call launches nothing). */
 int yapd_gemm_rmsnorm_qkv_rope_kv(const void* x, const void* ln_w, float eps, void* normed, const void* W_qkv,
                                   int M, int K, int n_heads, const float* cos_t, const float* sin_t, int max_pos,
                                   const int32_t* pos0, int bl, void* q_out, void* kv_pool, int64_t n_pages,

@@ -427,7 +427,8 @@ def gemm_rmsnorm_qkv_rope_kv(x: torch.Tensor, ln_w: torch.Tensor, eps: float, no
                              W_qkv: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor, pos0: torch.Tensor,
                              bl: int, q_out: torch.Tensor, pool: torch.Tensor, table: torch.Tensor) -> None:
     """Input RMSNorm of the residual stream ``x [M, K]`` into ``normed`` (a caller workspace of the
-    same shape), then :func:`gemm_qkv_rope_kv` on it (``yapd_gemm_rmsnorm_qkv_rope_kv``)."""
+    same shape), then :func:`gemm_qkv_rope_kv` on it (``yapd_gemm_rmsnorm_qkv_rope_kv``): two
+    launches, not a fused kernel."""
     dev = x.device
     require_cuda(x, "x", torch.bfloat16, dev)
     require(x.dim() == 2, "x must be [M, K]")
