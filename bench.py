@@ -293,7 +293,7 @@ def main():
         # one block costs K = 10 denoise steps + 1 commit forward (same shape)
         "committed_speech_tokens_per_s_est": round(tok_s / 11.0, 1),
         "projection_tflops": round(proj_flops / (ms * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": "gemm_dl_kernel<swiglu> (gate/up + SiLU*up, M=%d N=%d K=%d)" % (N, 2 * F, D),
+        "roofline": {"kernel": "gemm_pt_kernel<swiglu> (persistent; gate/up + SiLU*up, M=%d N=%d K=%d)" % (N, 2 * F, D),
                      "bound": "mfma", "achieved": round(tf_swiglu, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf_swiglu / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                      "peak_measured": round(peak_meas, 1), "frac_of_measured": round(tf_swiglu / peak_meas, 4),
