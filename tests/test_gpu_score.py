@@ -121,7 +121,8 @@ def assert_exact(res, ref):
 @pytest.mark.parametrize("layout", ["interleaved", "stacked"])
 @pytest.mark.parametrize("n_pairs,bl,V,tau,pitch", [(4, 16, 1000, 0.1, None), (8, 32, 8194, 3.0, None),
                                                     (3, 7, 8193, 0.1, 8194), (2, 64, 513, 0.5, 514),
-                                                    (1, 1, 3, 0.1, 4), (1, 2, 64, 3.0, None)])  # tail-only rows
+                                                    (1, 1, 3, 0.1, 4), (1, 2, 64, 3.0, None),  # tail-only rows
+                                                    (3, 40, 2050, 3.0, None)])  # ranks over > 32 positions
 def test_matches_oracle(dev, layout, n_pairs, bl, V, tau, pitch):
     res, ref, _ = run_both(dev, n_pairs=n_pairs, bl=bl, V=V, seed=n_pairs + bl, layout=layout, tau=tau,
                            pitch=pitch)
