@@ -62,8 +62,10 @@ class _Buffers:
 
 
 def _quant_bits_from(quant_bits: Optional[int]) -> int:
-    """0 (bf16 weights), 4 or 8.  Unset: ``CHATTERBOX_FLASH_MLX_QUANT_BITS`` (engines/mlx.py:224-240:
-    an unparsable value is ignored with a warning; the group size stays 64)."""
+    """0 (bf16 weights), 4 or 8.  Unset: ``CHATTERBOX_FLASH_MLX_QUANT_BITS`` as the Metal engine reads it
+    (engines/mlx.py:224-235: an unparsable value, or a width it does not quantise to, is ignored with a
+    warning); the widths it accepts but this engine does not build (2, 3, 6) raise, as does a group size
+    other than 64."""
     if quant_bits is None:
         raw = os.environ.get("CHATTERBOX_FLASH_MLX_QUANT_BITS", "").strip()
         if not raw:
@@ -72,6 +74,9 @@ def _quant_bits_from(quant_bits: Optional[int]) -> int:
             quant_bits = int(raw)
         except ValueError:
             logger.warning("Ignoring invalid CHATTERBOX_FLASH_MLX_QUANT_BITS=%r", raw)
+            return 0
+        if quant_bits not in (2, 3, 4, 6, 8):
+            logger.warning("Unsupported MLX quant bits=%d; skipping.", quant_bits)
             return 0
         group = int(os.environ.get("CHATTERBOX_FLASH_MLX_QUANT_GROUP", "64"))
         if group != 64:
