@@ -1017,42 +1017,50 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
 
 // ---------------------------------------------------------------------------
 // Persistent kernel for grids of at least two 256 x 256 tiles per CU (the
-// gate/up and speech-head GEMMs of the step): one workgroup per CU walks the
+// gate/up, speech-head and plain QKV GEMMs): one workgroup per CU walks the
 // tiles T = blockIdx.x, blockIdx.x + gridDim.x, ... (row-major, so a
-// workgroup keeps its XCD's column tiles of W), and the first k-tiles of the
-// next tile are requested before the current tile's epilogue, which then runs
-// while they are in flight.
+// workgroup keeps its XCD's column tiles of W), and the first two k-tiles of
+// the next tile are requested before the current tile's epilogue, which then
+// runs while they are in flight.
 //
 // Four waves, one per SIMD, each 128 x 128 of the tile (accumulators in the
-// AGPRs); BK 32 with four LDS stages (three k-tiles in flight).  Per-wave
-// cycle counters measured what decides the loop here: a burst of
-// direct-to-LDS loads stalls the in-order wave that issues it, while the same
-// loads spread one after every four MFMAs cost little, and the compiler's
-// scheduler does not keep such a spread (nor the loads ahead of a long
-// epilogue) on its own.  So each k-step is written as 16 groups of one MFMA,
-// at most one fragment read of the next k-step and every fourth group one
-// load of the k-tile three ahead (half of its loads per k-step), each group
-// fenced with sched_barrier.  The MFMA and the K order are those of the other
-// kernels, so a row's result does not depend on which kernel runs it.
+// AGPRs); BK 64 with two LDS stages.  A k-tile is four k-steps of 16 MFMAs;
+// each k-step reads the next k-step's fragments into the other register slot.
+// Stage s of k-tile kt may be refilled once every wave has read k-step 3's
+// fragments of kt (the barrier before k-step 3), so the loads of k-tile kt + 2
+// go out half in k-step 3 of kt and half early in k-step 0 of kt + 1, two
+// k-steps before the barrier that waits for them.  Against BK 32 with four
+// stages (three k-tiles in flight) this halves the barriers and requests each
+// operand row as whole 128-byte lines (the L2 requests of a 64-byte half-line
+// layout were twice the vendor library's for the same bytes): gate/up 265 ->
+// 242 us plain, QKV plain 105 -> 98 us, bit-identical.  Per-wave cycle
+// counters showed a burst of direct-to-LDS loads stalling the in-order wave
+// that issues it while the same loads spread over MFMAs cost little, and the
+// compiler keeps neither such a spread nor loads ahead of a long epilogue on
+// its own; so each k-step is written as 16 groups of one MFMA, at most one
+// fragment read and at most one load, each fenced with sched_barrier.  The
+// MFMA and the K order are those of the other kernels, so a row's result does
+// not depend on which kernel runs it.
 //
-// LDS rows hold BK = 32 bf16 (64 bytes); chunk c of row r sits in slot
-// c ^ ((r >> 2) & 3), so the 16 rows one 16-lane group of a fragment read
+// LDS rows hold BK = 64 bf16 (128 bytes); chunk c of row r sits in slot
+// c ^ ((r >> 1) & 7), so the 16 rows one 16-lane group of a fragment read
 // touches fill the 16 slots of a 256-byte bank line.  A 1 KB load
-// instruction covers 16 rows; lane i fills slot i % 4 of row i / 4.
+// instruction covers 8 rows; lane i fills slot i % 8 of row i / 8.
 namespace pt {
-constexpr int BM = 256, BN = 256, BK = 32, NS = 4, WAVES = 4, THREADS = 64 * WAVES;
+constexpr int BM = 256, BN = 256, BK = 64, NS = 2, WAVES = 4, THREADS = 64 * WAVES;
 constexpr int TM = 4, TN = 4;  // 32 x 32 MFMA tiles per wave
 constexpr int ROWB = BK * 2, CPR = BK / 8, RPI = 64 / CPR;
 constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
 constexpr int LA = BM / RPI / WAVES, LB = BN / RPI / WAVES, LPT = LA + LB, HL = LPT / 2;
 constexpr int LDS = NS * STAGE;
 constexpr int NM = TM * TN, NR = TM + TN;
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 // Stores per lane of one full tile's epilogue (16-byte runs): swiglu 16, plain 32.
 template <int EPI>
 constexpr int tile_stores() {
   return EPI == kEpiSwiglu ? TM * (TN / 2) * 2 : TM * TN * 2;
 }
+constexpr int kStoresCap(int n) { return n < 63 ? n : 63; }
 
 // The transposed product leaves lane l and lane l + 32 with the 4-column runs
 // 8 r + 0..3 and 8 r + 4..7 of the same token.  Given a lane's runs of r = 2 h
@@ -1075,7 +1083,7 @@ __device__ __forceinline__ void stage_barrier() {
 
 template <int EPI, int AM>
 __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p) {
-  constexpr int BM = pt::BM, BN = pt::BN, BK = pt::BK, NS = pt::NS, WAVES = pt::WAVES;
+  constexpr int BM = pt::BM, BN = pt::BN, BK = pt::BK;
   constexpr int TM = pt::TM, TN = pt::TN, ROWB = pt::ROWB, CPR = pt::CPR, RPI = pt::RPI;
   constexpr int A_BYTES = pt::A_BYTES, STAGE = pt::STAGE, LA = pt::LA, LB = pt::LB, LPT = pt::LPT, HL = pt::HL;
   constexpr int NM = pt::NM, NR = pt::NR;
@@ -1091,42 +1099,67 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
   const int ntx = (p.N + BN - 1) / BN;
   const int ntiles = ntx * ((p.M + BM - 1) / BM);
 
-  // Per-lane sources of this wave's LA + LB loads of a tile (k offset added per k-tile).
-  const uint16_t* a_src[LA];
-  const uint16_t* b_src[LB];
+  // Load sources: a uniform tile base (SGPRs) plus a 32-bit byte offset per
+  // load, which halves the address registers of 64-bit row pointers.  With
+  // the token shift, a row reads either the hidden row before it or its
+  // block's shift_ctx row: bit 0 of the offset (offsets are multiples of 16)
+  // selects the shift_ctx base.
+  uint32_t a_ofs[LA], b_ofs[LB];
+  const char* a_base = nullptr;
+  const char* s_base = nullptr;
+  const char* w_base = nullptr;
   auto set_tile = [&](int T) {
     const int m0 = (T / ntx) * BM, n0 = (T % ntx) * BN;
+    if constexpr (AM == kAShift) {
+      // relative to hidden row m0 - 1 and to shift_ctx row m0 / bl
+      a_base = reinterpret_cast<const char*>(p.A + (static_cast<int64_t>(m0) - 1) * p.lda);
+      s_base = reinterpret_cast<const char*>(p.shift_ctx + static_cast<int64_t>(m0 / p.shift_bl) * p.K);
+    } else {
+      a_base = reinterpret_cast<const char*>(p.A + static_cast<int64_t>(m0) * p.lda);
+    }
+    w_base = reinterpret_cast<const char*>(p.W + static_cast<int64_t>(n0) * p.ldw);
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
       const int r = (wave * LA + j) * RPI + lane / CPR;
       const int c = (lane % CPR) ^ swz(r);
-      a_src[j] = a_row_ptr<AM>(p, min(m0 + r, p.M - 1)) + 8 * c;
+      const int m = min(m0 + r, p.M - 1);
+      if constexpr (AM == kAShift) {
+        const int blk = m / p.shift_bl;
+        a_ofs[j] = m - blk * p.shift_bl == 0
+                       ? static_cast<uint32_t>(((static_cast<int64_t>(blk - m0 / p.shift_bl) * p.K + 8 * c) * 2) | 1)
+                       : static_cast<uint32_t>((static_cast<int64_t>(m - m0) * p.lda + 8 * c) * 2);
+      } else {
+        a_ofs[j] = static_cast<uint32_t>((static_cast<int64_t>(m - m0) * p.lda + 8 * c) * 2);
+      }
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
       const int r = (wave * LB + j) * RPI + lane / CPR;
       const int c = (lane % CPR) ^ swz(r);
-      b_src[j] = p.W + static_cast<int64_t>(min(n0 + r, p.N - 1)) * p.ldw + 8 * c;
+      b_ofs[j] = static_cast<uint32_t>((static_cast<int64_t>(min(n0 + r, p.N - 1) - n0) * p.ldw + 8 * c) * 2);
     }
   };
-  // loads j0 .. j0 + n - 1 of this wave's LPT for k-tile kt (A loads first)
-  auto issue = [&](int kt, int stage, int j0, int n) {
+  // load j of this wave's LPT for k-tile kt into stage (A loads first)
+  auto issue1 = [&](int kt, int stage, int j) {
     const int k = kt * BK;
-    char* a_dst = lds + stage * STAGE + wave * LA * 1024;
-    char* b_dst = lds + stage * STAGE + A_BYTES + wave * LB * 1024;
-#pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      if (j < j0 || j >= j0 + n) continue;
-      if (j < LA) {
-        load_lds16(a_src[j] + k, a_dst + j * 1024);
+    if (j < LA) {
+      const char* src;
+      if constexpr (AM == kAShift) {
+        src = ((a_ofs[j] & 1u) ? s_base : a_base) + 2 * k + (a_ofs[j] & ~1u);
       } else {
-        load_lds16(b_src[j - LA] + k, b_dst + (j - LA) * 1024);
+        src = a_base + 2 * k + a_ofs[j];
       }
+      load_lds16(reinterpret_cast<const uint16_t*>(src), lds + stage * STAGE + (wave * LA + j) * 1024);
+    } else {
+      load_lds16(reinterpret_cast<const uint16_t*>(w_base + 2 * k + b_ofs[j - LA]),
+                 lds + stage * STAGE + A_BYTES + (wave * LB + j - LA) * 1024);
     }
   };
   auto prologue = [&]() {
 #pragma unroll
-    for (int s = 0; s + 1 < NS; ++s) issue(s, s, 0, LPT);
+    for (int s = 0; s < pt::NS; ++s)
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) issue1(s, s, j);
   };
 
   f32x16_t acc[TM][TN];
@@ -1145,21 +1178,22 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
     }
   };
   // One k-step: the MFMAs on fragment slot `slot`; with rd the fragments of
-  // the next k-step (rstage, rks) into the other slot; with nl = HL the loads
-  // lj0 .. lj0 + HL - 1 of k-tile lkt into stage lstage.  Both epilogues use
-  // the transposed product (W x A^T: a lane holds one token and 4-column runs).
+  // k-step rks of stage rstage into the other slot; with nl > 0 the loads
+  // lj0 .. lj0 + nl - 1 of k-tile lkt into stage lstage, one after every
+  // NM / nl MFMAs.  Both epilogues use the transposed product (W x A^T: a
+  // lane holds one token and 4-column runs).
   auto kstep = [&](int slot, bool rd, int rstage, int rks, int nl, int lkt, int lstage, int lj0) {
 #pragma unroll
     for (int r = 0; r < NM; ++r) {
       const int i = r % TM, j = r / TM;
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0);
       if (rd && r < NR) frag_rd(rstage, rks, slot ^ 1, r);
-      if (nl > 0 && r % (NM / HL) == NM / HL - 1) issue(lkt, lstage, lj0 + r / (NM / HL), 1);
+      if (nl > 0 && r % (NM / nl) == NM / nl - 1) issue1(lkt, lstage, lj0 + r / (NM / nl));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  const int tok = lane & 31, csub = 4 * (lane >> 5);
+  const int tok = lane & 31;
   const bool vec_ok = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
   int T = blockIdx.x;
   set_tile(T);
@@ -1175,35 +1209,41 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-    // k-tile 0 has landed: k-tiles 1 and 2 (and the stores of a full previous
-    // epilogue, issued after them) may stay in flight
-    constexpr int kAfterFull = 2 * LPT + pt::tile_stores<EPI>() < 63 ? 2 * LPT + pt::tile_stores<EPI>() : 63;
+    // k-tile 0 has landed: k-tile 1 (and the stores of a full previous
+    // epilogue, issued after it) may stay in flight
     if (after_full) {
-      pt::stage_barrier<kAfterFull>();
+      pt::stage_barrier<pt::kStoresCap(LPT + pt::tile_stores<EPI>())>();
     } else {
-      pt::stage_barrier<2 * LPT>();
+      pt::stage_barrier<LPT>();
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) frag_rd(0, 0, 0, r);
-    int stage = 0, kt = 0;
-    // steady state: k-tile kt + 3 requested in two halves over k-tile kt
-    for (; kt + NS - 1 < kt_n; ++kt) {
-      const int next = (stage + 1) & 3, lst = (stage + 3) & 3;
-      kstep(0, true, stage, 1, HL, kt + 3, lst, 0);
-      // k-tile kt + 1 landed: k-tile kt + 2 and the first half of kt + 3 may stay in flight
-      pt::stage_barrier<(NS - 3) * LPT + HL>();
-      kstep(1, true, next, 0, HL, kt + 3, lst, HL);
-      stage = next;
-    }
-    // the last k-tiles are all requested
-    for (; kt + 1 < kt_n; ++kt) {
-      const int next = (stage + 1) & 3;
-      kstep(0, true, stage, 1, 0, 0, 0, 0);
+    // k-tile 0 (k-tile 1 came with the prologue)
+    kstep(0, true, 0, 1, 0, 0, 0, 0);
+    kstep(1, true, 0, 2, 0, 0, 0, 0);
+    kstep(0, true, 0, 3, 0, 0, 0, 0);
+    // k-tile 1 has landed (the stores may stay in flight); stage 0 is free
+    if (after_full) {
+      pt::stage_barrier<pt::kStoresCap(pt::tile_stores<EPI>())>();
+    } else {
       pt::stage_barrier<0>();
-      kstep(1, true, next, 0, 0, 0, 0, 0);
-      stage = next;
     }
-    kstep(0, true, stage, 1, 0, 0, 0, 0);
+    kstep(1, true, 1, 0, kt_n > 2 ? HL : 0, 2, 0, 0);
+    int kt = 1;
+    for (; kt + 1 < kt_n; ++kt) {
+      const int s = kt & 1;
+      // the other half of k-tile kt + 1's loads, two k-steps ahead of the barrier
+      kstep(0, true, s, 1, LPT - HL, kt + 1, s ^ 1, HL);
+      kstep(1, true, s, 2, 0, 0, 0, 0);
+      kstep(0, true, s, 3, 0, 0, 0, 0);
+      // k-tile kt + 1 has landed and every wave has read stage s
+      pt::stage_barrier<0>();
+      kstep(1, true, s ^ 1, 0, kt + 2 < kt_n ? HL : 0, kt + 2, s, 0);
+    }
+    // the last k-tile
+    kstep(0, true, kt & 1, 1, 0, 0, 0, 0);
+    kstep(1, true, kt & 1, 2, 0, 0, 0, 0);
+    kstep(0, true, kt & 1, 3, 0, 0, 0, 0);
     pt::stage_barrier<0>();
     // No LDS read is left in this tile: request the next tile's first
     // k-tiles, kept ahead of the epilogue so they land while it runs.
@@ -1475,7 +1515,7 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   // tile's first loads (gate/up + SiLU at M = 16384: 318 -> 266 us on one box,
   // bit-identical; the speech head likewise).
   if constexpr (BQ == 0 && (EPI == kEpiSwiglu || EPI == kEpiStore)) {
-    if (big_tiles >= 2 * cu_count() && p.K >= pt::BK * pt::NS) {
+    if (big_tiles >= 2 * cu_count() && p.K >= pt::BK * pt::NS && p.K % pt::BK == 0) {
       if constexpr (EPI == kEpiStore) {
         // the head's last 2 columns (N = 8194) as below: their own one-wave launch
         const int tail = p.N % 256;
