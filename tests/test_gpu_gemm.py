@@ -28,9 +28,9 @@ def rel_err(out, ref):
 # one 128 x 128 tile per CU, which runs three LDS stages: K = 64 / 128 / 192 give one, two and three
 # k-tiles (the stage hand-off's short and tail cases); (3000, 1000, 4096) a ragged grid of that kind.
 # Grids of at least two 256 x 256 tiles per CU take the persistent kernel: (4100, 8192, 1024) with a
-# partial last row tile, (8000, 4196, 128) with a 100-column last tile and the shortest K it takes (four
-# 32-wide k-tiles: no steady-state iteration after the first), (8192, 8194, 192) with the 2-column tail
-# split off to its own launch.
+# partial last row tile, (8000, 4196, 128) with a 100-column last tile and the shortest K it takes (two
+# 64-wide k-tiles: no steady-state iteration), (8192, 8194, 192) with the 2-column tail split off to its
+# own launch and three k-tiles (one steady-state iteration, no loads of a fourth).
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 3072, 1024), (1024, 1024, 4096), (37, 8194, 1024),
                                    (16384 // 8, 8192, 1024), (2000, 8192, 1024), (4100, 4096, 2048),
                                    (3072, 1024, 64), (3072, 1024, 128), (3072, 1024, 192), (3000, 1000, 4096),
