@@ -107,7 +107,9 @@ def test_gemm_head_shift(dev, rows):
 # 180 x 32 rows: large-tile path.  6 heads at 320 x 32 rows: 256-column tiles
 # straddle the q/k boundary (q = columns [0, 384)) and one tile holds only V
 # columns (no RoPE rows staged); 2 heads: q, k and v inside one small tile.
-@pytest.mark.parametrize("rows,H", [(3, 16), (180, 16), (320, 6), (3, 2)])
+# 512 x 32 rows (the step's shape) and 515 x 32: the persistent kernel, in XCD
+# row bands and, with 65 row tiles (the last one partial), row-major.
+@pytest.mark.parametrize("rows,H", [(3, 16), (180, 16), (320, 6), (3, 2), (512, 16), (515, 16)])
 def test_gemm_qkv_rope_kv(dev, rows, H):
     D, bl = 1024, 32
     M = rows * bl

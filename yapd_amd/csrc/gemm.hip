@@ -1017,11 +1017,13 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dlq_kernel(const GemmParams p
 
 // ---------------------------------------------------------------------------
 // Persistent kernel for grids of at least two 256 x 256 tiles per CU (the
-// gate/up, speech-head and plain QKV GEMMs): one workgroup per CU walks the
-// tiles T = blockIdx.x, blockIdx.x + gridDim.x, ... (row-major, so a
-// workgroup keeps its XCD's column tiles of W), and the first two k-tiles of
+// gate/up, QKV and speech-head GEMMs): one workgroup per CU walks the tiles
+// T = blockIdx.x, blockIdx.x + gridDim.x, ... (row-major, so a workgroup
+// keeps its XCD's column tiles of W; QKV in XCD row bands, columns fastest,
+// so each A row block is fetched by one XCD), and the first two k-tiles of
 // the next tile are requested before the current tile's epilogue, which then
-// runs while they are in flight.
+// runs while they are in flight (QKV: after it, as its epilogue stages the
+// rows' positions, pages and RoPE columns in LDS).
 //
 // Four waves, one per SIMD, each 128 x 128 of the tile (accumulators in the
 // AGPRs); BK 64 with two LDS stages.  A k-tile is four k-steps of 16 MFMAs;
@@ -1089,15 +1091,36 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
   constexpr int NM = pt::NM, NR = pt::NR;
   using pt::pair_runs;
   using pt::swz;
-  static_assert(EPI == kEpiSwiglu || EPI == kEpiStore, "persistent kernel epilogues: swiglu, plain store");
+  static_assert(EPI == kEpiSwiglu || EPI == kEpiStore || EPI == kEpiQkv,
+                "persistent kernel epilogues: swiglu, plain store, qkv");
+  using TT = Tile<BM, BN, BK, 2, 2>;  // the wave layout, for the shared qkv epilogue
+  static_assert(EPI != kEpiQkv || qkv_lds_bytes<TT>() <= pt::LDS, "qkv epilogue LDS");
   extern __shared__ __attribute__((aligned(16))) uint16_t dyn_lds[];
   char* lds = reinterpret_cast<char*>(dyn_lds);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
   const int kt_n = p.K / BK;
-  const int ntx = (p.N + BN - 1) / BN;
-  const int ntiles = ntx * ((p.M + BM - 1) / BM);
+  const int ntx = (p.N + BN - 1) / BN, nty = (p.M + BM - 1) / BM;
+  const int ntiles = ntx * nty;
+  // Tile k of this workgroup.  Row-major: T = blockIdx.x + k * gridDim.x.  QKV
+  // bands (workgroups go round-robin to the 8 XCDs): XCD x takes row tiles
+  // [x R, (x + 1) R), R = nty / 8, walked columns fastest by its workgroups.
+  const bool band = EPI == kEpiQkv && nty % 8 == 0 && gridDim.x % 8 == 0;
+  auto tile_at = [&](int k, int& m0, int& n0) {
+    if (band) {
+      const int g8 = gridDim.x / 8, t = blockIdx.x / 8 + k * g8, rows = nty / 8;
+      if (t >= rows * ntx) return false;
+      m0 = ((blockIdx.x % 8) * rows + t / ntx) * BM;
+      n0 = (t % ntx) * BN;
+      return true;
+    }
+    const int T = blockIdx.x + k * gridDim.x;
+    if (T >= ntiles) return false;
+    m0 = (T / ntx) * BM;
+    n0 = (T % ntx) * BN;
+    return true;
+  };
 
   // Load sources: a uniform tile base (SGPRs) plus a 32-bit byte offset per
   // load, which halves the address registers of 64-bit row pointers.  With
@@ -1108,8 +1131,7 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
   const char* a_base = nullptr;
   const char* s_base = nullptr;
   const char* w_base = nullptr;
-  auto set_tile = [&](int T) {
-    const int m0 = (T / ntx) * BM, n0 = (T % ntx) * BN;
+  auto set_tile = [&](int m0, int n0) {
     if constexpr (AM == kAShift) {
       // relative to hidden row m0 - 1 and to shift_ctx row m0 / bl
       a_base = reinterpret_cast<const char*>(p.A + (static_cast<int64_t>(m0) - 1) * p.lda);
@@ -1195,14 +1217,17 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
 
   const int tok = lane & 31;
   const bool vec_ok = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
-  int T = blockIdx.x;
-  set_tile(T);
-  prologue();
+  int m0 = 0, n0 = 0;
+  if (tile_at(0, m0, n0)) {
+    set_tile(m0, n0);
+    prologue();
+  }
   // Stores the previous tile's epilogue surely issued after this tile's
-  // prologue (0 for the first tile and after a partial tile).
+  // prologue (0 for the first tile, after a partial tile, and for QKV).
   bool after_full = false;
-  for (; T < ntiles; T += gridDim.x) {
-    const int m0 = (T / ntx) * BM, n0 = (T % ntx) * BN;
+  for (int kti = 0; tile_at(kti, m0, n0); ++kti) {
+    // qkv: this tile's row positions and pages, loaded while the k-loop runs
+    const RowMeta rm = EPI == kEpiQkv ? qkv_row_meta<TT>(p, m0, tid) : RowMeta{0, 0};
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1247,9 +1272,20 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
     pt::stage_barrier<0>();
     // No LDS read is left in this tile: request the next tile's first
     // k-tiles, kept ahead of the epilogue so they land while it runs.
-    const int Tn = T + gridDim.x;
-    if (Tn < ntiles) {
-      set_tile(Tn);
+    int m1 = 0, n1 = 0;
+    const bool next = tile_at(kti + 1, m1, n1);
+    if constexpr (EPI == kEpiQkv) {
+      kstep(1, false, 0, 0, 0, 0, 0, 0);
+      finish_tile<TT, kEpiQkv>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
+      __syncthreads();  // the epilogue's LDS reads are done before the next tile's loads land there
+      if (next) {
+        set_tile(m1, n1);
+        prologue();
+      }
+      continue;
+    }
+    if (next) {
+      set_tile(m1, n1);
       prologue();
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1514,7 +1550,7 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   // the persistent kernel, which overlaps each tile's epilogue with the next
   // tile's first loads (gate/up + SiLU at M = 16384: 318 -> 266 us on one box,
   // bit-identical; the speech head likewise).
-  if constexpr (BQ == 0 && (EPI == kEpiSwiglu || EPI == kEpiStore)) {
+  if constexpr (BQ == 0 && (EPI == kEpiSwiglu || EPI == kEpiStore || EPI == kEpiQkv)) {
     if (big_tiles >= 2 * cu_count() && p.K >= pt::BK * pt::NS && p.K % pt::BK == 0) {
       if constexpr (EPI == kEpiStore) {
         // the head's last 2 columns (N = 8194) as below: their own one-wave launch
