@@ -2,7 +2,9 @@
 // row kernel.
 //
 // C[M, N] = A[M, K] * W[N, K]^T (nn.Linear layout), fp32 accumulation on
-// v_mfma_f32_32x32x16_bf16.  Large M: `gemm_dl_kernel`, a 256 x 256 tile of
+// v_mfma_f32_32x32x16_bf16.  Grids of at least two 256 x 256 tiles per CU
+// (gate/up, QKV, the speech head): `gemm_pt_kernel`, one persistent 4-wave
+// workgroup per CU.  Other large M: `gemm_dl_kernel`, a 256 x 256 tile of
 // 8 waves (128 x 64 each) whose A and W k-slices go global -> LDS by direct
 // loads into two 64 KB stages.  Small M: the same kernel on one-wave 64 x 64
 // tiles with three stages.  Mid M: the same kernel on 128 x 128 tiles of 8
