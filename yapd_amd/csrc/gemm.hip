@@ -3,8 +3,9 @@
 //
 // C[M, N] = A[M, K] * W[N, K]^T (nn.Linear layout), fp32 accumulation on
 // v_mfma_f32_32x32x16_bf16.  Grids of at least two 256 x 256 tiles per CU
-// (gate/up, QKV, the speech head): `gemm_pt_kernel`, one persistent 4-wave
-// workgroup per CU.  Other large M: `gemm_dl_kernel`, a 256 x 256 tile of
+// (gate/up, QKV, the speech head), or one with the plain or residual epilogue
+// (o, down): `gemm_pt_kernel`, one persistent 4-wave workgroup per CU.  Other
+// large M: `gemm_dl_kernel`, a 256 x 256 tile of
 // 8 waves (128 x 64 each) whose A and W k-slices go global -> LDS by direct
 // loads into two 64 KB stages.  Small M: the same kernel on one-wave 64 x 64
 // tiles with three stages.  Mid M: the same kernel on 128 x 128 tiles of 8
@@ -352,7 +353,11 @@ __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f3
   // With ADD, all of this thread's residual chunks are requested at once
   // (the accumulators are dead now), so they cost one round trip, which the
   // barrier waits for; loads placed after stores to the same array would
-  // otherwise run one round trip per chunk.
+  // otherwise run one round trip per chunk.  Addresses: the tile's uniform
+  // base plus a 32-bit byte offset per chunk (a tile spans far less than
+  // 4 GiB), half the registers of 64-bit pointers.
+  const char* const c_base = reinterpret_cast<const char*>(p.C + static_cast<int64_t>(m0) * p.ldc + n0);
+  auto c_ofs = [&](int r, int cc) { return static_cast<uint32_t>((r * p.ldc + cc) * 2); };
   u32x4_t res[ADD ? ITER : 1];
   if constexpr (ADD) {
 #pragma unroll
@@ -360,19 +365,22 @@ __device__ __forceinline__ void store_tile_via_lds(const GemmParams& p, const f3
       const int idx = tid + it * T::THREADS;
       const int r = idx / CPR, cc = (idx % CPR) * 8;
       const int m = m0 + r, n = n0 + cc;
-      if (vec_ok && m < p.M && n + 8 <= p.N)
-        res[it] = *reinterpret_cast<const u32x4_t*>(p.C + static_cast<int64_t>(m) * p.ldc + n);
+      if (vec_ok && m < p.M && n + 8 <= p.N) res[it] = *reinterpret_cast<const u32x4_t*>(c_base + c_ofs(r, cc));
     }
   }
   __syncthreads();
+  // the stores' indices from an opaque copy of tid: recomputed here, so the
+  // loads' offsets need not stay live beside the residual chunks
+  int tid_s = tid;
+  if constexpr (ADD) asm volatile("" : "+v"(tid_s));
 #pragma unroll
   for (int it = 0; it < ITER; ++it) {
-    const int idx = tid + it * T::THREADS;
+    const int idx = tid_s + it * T::THREADS;
     const int r = idx / CPR, cc = (idx % CPR) * 8;
     const int m = m0 + r, n = n0 + cc;
     if (m >= p.M || n >= p.N) continue;
     const uint16_t* src = lds + r * CP + cc;
-    uint16_t* dst = p.C + static_cast<int64_t>(m) * p.ldc + n;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(const_cast<char*>(c_base) + c_ofs(r, cc));
     if (vec_ok && n + 8 <= p.N) {
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
       if constexpr (ADD) {
@@ -1057,6 +1065,11 @@ constexpr int ROWB = BK * 2, CPR = BK / 8, RPI = 64 / CPR;
 constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
 constexpr int LA = BM / RPI / WAVES, LB = BN / RPI / WAVES, LPT = LA + LB, HL = LPT / 2;
 constexpr int LDS = NS * STAGE;
+// The residual epilogue stages the C tile in LDS (rows padded by 16 bytes).
+template <int EPI>
+constexpr int lds_bytes() {
+  return EPI == kEpiResidual && BM * (BN + 8) * 2 > LDS ? BM * (BN + 8) * 2 : LDS;
+}
 constexpr int NM = TM * TN, NR = TM + TN;
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 // Stores per lane of one full tile's epilogue (16-byte runs): swiglu 16, plain 32.
@@ -1093,8 +1106,8 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
   constexpr int NM = pt::NM, NR = pt::NR;
   using pt::pair_runs;
   using pt::swz;
-  static_assert(EPI == kEpiSwiglu || EPI == kEpiStore || EPI == kEpiQkv,
-                "persistent kernel epilogues: swiglu, plain store, qkv");
+  static_assert(EPI == kEpiSwiglu || EPI == kEpiStore || EPI == kEpiQkv || EPI == kEpiResidual,
+                "persistent kernel epilogues: swiglu, plain store, qkv, residual");
   using TT = Tile<BM, BN, BK, 2, 2>;  // the wave layout, for the shared qkv epilogue
   static_assert(EPI != kEpiQkv || qkv_lds_bytes<TT>() <= pt::LDS, "qkv epilogue LDS");
   extern __shared__ __attribute__((aligned(16))) uint16_t dyn_lds[];
@@ -1105,10 +1118,12 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
   const int kt_n = p.K / BK;
   const int ntx = (p.N + BN - 1) / BN, nty = (p.M + BM - 1) / BM;
   const int ntiles = ntx * nty;
-  // Tile k of this workgroup.  Row-major: T = blockIdx.x + k * gridDim.x.  QKV
-  // bands (workgroups go round-robin to the 8 XCDs): XCD x takes row tiles
-  // [x R, (x + 1) R), R = nty / 8, walked columns fastest by its workgroups.
-  const bool band = EPI == kEpiQkv && nty % 8 == 0 && gridDim.x % 8 == 0;
+  // Tile k of this workgroup.  Row-major: T = blockIdx.x + k * gridDim.x.
+  // Bands (QKV, and grids the launcher marks: single-round ones and narrow
+  // long-K ones; workgroups go round-robin to the 8 XCDs): XCD x takes row
+  // tiles [x R, (x + 1) R), R = nty / 8, walked columns fastest by its
+  // workgroups, so each A row block is fetched by one XCD.
+  const bool band = (EPI == kEpiQkv || p.xcd_band != 0) && nty % 8 == 0 && gridDim.x % 8 == 0;
   auto tile_at = [&](int k, int& m0, int& n0) {
     if (band) {
       const int g8 = gridDim.x / 8, t = blockIdx.x / 8 + k * g8, rows = nty / 8;
@@ -1204,13 +1219,16 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
   // One k-step: the MFMAs on fragment slot `slot`; with rd the fragments of
   // k-step rks of stage rstage into the other slot; with nl > 0 the loads
   // lj0 .. lj0 + nl - 1 of k-tile lkt into stage lstage, one after every
-  // NM / nl MFMAs.  Both epilogues use the transposed product (W x A^T: a
-  // lane holds one token and 4-column runs).
+  // NM / nl MFMAs.  The register epilogues (swiglu, plain, qkv) use the
+  // transposed product (W x A^T: a lane holds one token and 4-column runs);
+  // the residual epilogue, staged through LDS, the direct one.
   auto kstep = [&](int slot, bool rd, int rstage, int rks, int nl, int lkt, int lstage, int lj0) {
 #pragma unroll
     for (int r = 0; r < NM; ++r) {
       const int i = r % TM, j = r / TM;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0);
+      acc[i][j] = EPI == kEpiResidual
+                      ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0)
+                      : __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0);
       if (rd && r < NR) frag_rd(rstage, rks, slot ^ 1, r);
       if (nl > 0 && r % (NM / nl) == NM / nl - 1) issue1(lkt, lstage, lj0 + r / (NM / nl));
       __builtin_amdgcn_sched_barrier(0);
@@ -1276,9 +1294,15 @@ __global__ __launch_bounds__(pt::THREADS) void gemm_pt_kernel(const GemmParams p
     // k-tiles, kept ahead of the epilogue so they land while it runs.
     int m1 = 0, n1 = 0;
     const bool next = tile_at(kti + 1, m1, n1);
-    if constexpr (EPI == kEpiQkv) {
+    if constexpr (EPI == kEpiQkv || EPI == kEpiResidual) {
+      // epilogues that use LDS: the next tile's loads follow them
       kstep(1, false, 0, 0, 0, 0, 0, 0);
-      finish_tile<TT, kEpiQkv>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane, tid);
+      // The epilogue's addresses depend only on the thread; computed from
+      // these opaque copies they stay here instead of being hoisted out of
+      // the tile loop and held (spilled) across the k-loop.
+      int tid_e = tid, lane_e = lane;
+      asm volatile("" : "+v"(tid_e), "+v"(lane_e));
+      finish_tile<TT, EPI>(p, acc, dyn_lds, rm, m0, n0, wm, wn, lane_e, tid_e);
       __syncthreads();  // the epilogue's LDS reads are done before the next tile's loads land there
       if (next) {
         set_tile(m1, n1);
@@ -1516,14 +1540,14 @@ int launch_pt(const GemmParams& p, hipStream_t st, int cus) {
   if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
   if (dev < 0 || dev >= 64 || !lds_set[dev]) {
     if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_pt_kernel<EPI, AM>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, pt::LDS),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, pt::lds_bytes<EPI>()),
                            "gemm_pt_kernel LDS attribute"))
       return rc;
     if (dev >= 0 && dev < 64) lds_set[dev] = true;
   }
   const int64_t tiles = static_cast<int64_t>((p.M + pt::BM - 1) / pt::BM) * ((p.N + pt::BN - 1) / pt::BN);
   const int grid = static_cast<int>(tiles < cus ? tiles : cus);
-  hipLaunchKernelGGL((gemm_pt_kernel<EPI, AM>), dim3(grid), dim3(pt::THREADS), pt::LDS, st, p);
+  hipLaunchKernelGGL((gemm_pt_kernel<EPI, AM>), dim3(grid), dim3(pt::THREADS), pt::lds_bytes<EPI>(), st, p);
   YAPD_LAUNCH_CHECK("gemm_pt_kernel launch");
   return YAPD_OK;
 }
@@ -1548,12 +1572,19 @@ int launch_gemm(GemmParams p, hipStream_t st) {
   // tiles the 128 x 128 kernel is still faster) or, for the quantised path,
   // once they give one workgroup per CU.
   const int64_t big_tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
-  // At least two tiles per CU, bf16 W and the swiglu or plain-store epilogue:
-  // the persistent kernel, which overlaps each tile's epilogue with the next
-  // tile's first loads (gate/up + SiLU at M = 16384: 318 -> 266 us on one box,
-  // bit-identical; the speech head likewise).
-  if constexpr (BQ == 0 && (EPI == kEpiSwiglu || EPI == kEpiStore || EPI == kEpiQkv)) {
-    if (big_tiles >= 2 * cu_count() && p.K >= pt::BK * pt::NS && p.K % pt::BK == 0) {
+  // bf16 W and at least two tiles per CU, or for the plain and residual
+  // epilogues at least one: the persistent kernel, which overlaps each tile's
+  // epilogue with the next tile's first loads where the epilogue works from
+  // registers (gate/up + SiLU at M = 16384: 318 -> 266 us on one box,
+  // bit-identical; the speech head likewise).  On single-round grids its XCD
+  // bands beat the 8-wave kernel's (plain down at M = 16384: 124.2 -> 112.8 us,
+  // o 36.3 -> 34.9 us, bit-identical).  Banded: single-round grids and, for
+  // the residual epilogue, narrow long-K ones (down at M > 16384, as below).
+  if constexpr (BQ == 0 && (EPI == kEpiSwiglu || EPI == kEpiStore || EPI == kEpiQkv || EPI == kEpiResidual)) {
+    const int64_t min_tiles = EPI == kEpiStore || EPI == kEpiResidual ? cu_count() : 2 * cu_count();
+    if (big_tiles >= min_tiles && p.K >= pt::BK * pt::NS && p.K % pt::BK == 0) {
+      const bool narrow_long = (p.N + 255) / 256 <= 8 && p.K >= 2048;
+      p.xcd_band = big_tiles <= cu_count() || (EPI == kEpiResidual && narrow_long) ? 1 : 0;
       if constexpr (EPI == kEpiStore) {
         // the head's last 2 columns (N = 8194) as below: their own one-wave launch
         const int tail = p.N % 256;
