@@ -33,7 +33,8 @@ extern "C" {
 const char* yapd_last_error(void);
 
 /* ABI revision of this library (bumped on any signature or struct layout
- * change; 3 added the quantised-weight fields of yapd_t3_layer). */
+ * change; 3 added the quantised-weight fields of yapd_t3_layer, 4 the wdq
+ * buffer of yapd_t3_workspace). */
 int yapd_abi_version(void);
 
 /* ------------------------------------------------------------------------ *
@@ -206,6 +207,16 @@ int yapd_qgemm_affine(const void* A, int64_t lda, const uint32_t* w_packed, cons
                       const void* biases, int bits, int group_size, int M, int N, int K, void* C, int64_t ldc,
                       void* stream);
 
+/* (d) The weights yapd_qgemm_affine multiplies by: W_out[N, K] (bf16, row
+ * pitch K, 16-byte aligned) = bf16(scale*q + bias), the dequantisation of
+ * mlx.core.dequantize on the layout of engines/mlx.py:221-255 (the same
+ * arithmetic as yapd_qgemm_affine's W loader, so yapd_gemm_bf16 on W_out
+ * equals yapd_qgemm_affine bit for bit).  For many rows the dequantise-once
+ * route is the faster one: the fused kernel dequantises each W tile again for
+ * every tile row.  bits 4 or 8, group_size 64, K a multiple of 64. */
+int yapd_dequant_affine(const uint32_t* w_packed, const void* scales, const void* biases, int bits,
+                        int group_size, int N, int K, void* W_out, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * Whole block forward: one call runs the n_layers decoder layers and the
  * final norm (engines/flashinfer.py:_block_forward_fused :970-1065 /
@@ -269,6 +280,14 @@ typedef struct yapd_t3_workspace {
   float* part_o;
   float* part_ml;
   int n_slots;
+  /* Optional (NULL: unused), for quantised layers: bf16 scratch of wdq_elems
+   * >= 3*H*64*D + D*H*64 + 2*F*D + D*F elements, 16-byte aligned.  With it,
+   * a quantised layer over at least 4096 rows dequantises its four weights
+   * into it (one yapd_dequant_affine pass) and runs the bf16 kernels, whose
+   * results equal the fused quantised kernels' bit for bit; fewer rows, or
+   * no buffer, run the fused kernels on the codes. */
+  void* wdq;
+  int64_t wdq_elems;
 } yapd_t3_workspace;
 
 /* block_emb [rows*bl, D] is not modified; pos0 [rows] (device) is each row's

@@ -50,7 +50,7 @@ def test_ctypes_signatures_cover_header():
 
 def test_abi_version_and_empty_error():
     lib = kernels.load_library()
-    assert lib.yapd_abi_version() == 3  # the layout of yapd_t3_layer in include/yapd_t3.h
+    assert lib.yapd_abi_version() == 4  # the layouts of yapd_t3_layer and yapd_t3_workspace in include/yapd_t3.h
     assert isinstance(lib.yapd_last_error(), bytes)
 
 
@@ -98,6 +98,10 @@ REJECTS = [
     ("yapd_rmsnorm", (None, None, P, P, 1e-5, 0, 1024, P, None), b"empty"),
     ("yapd_qgemm_affine", (P, 1024, P, P, P, 3, 64, 64, 1024, 1024, P, 1024, None), b"bits must be 4 or 8"),
     ("yapd_qgemm_affine", (P, 1024, P, P, P, 4, 32, 64, 1024, 1024, P, 1024, None), b"group_size must be 64"),
+    ("yapd_dequant_affine", (P, P, P, 3, 64, 1024, 1024, P, None), b"bits must be 4 or 8"),
+    ("yapd_dequant_affine", (P, P, P, 4, 32, 1024, 1024, P, None), b"group_size must be 64"),
+    ("yapd_dequant_affine", (P, P, P, 4, 64, 1024, 1000, P, None), b"K % 64 == 0"),
+    ("yapd_dequant_affine", (P, P, P, 8, 64, 1024, 1024, P + 4, None), b"outputs must be non-NULL and 16-byte"),
     ("yapd_attn_paged_block", (P, P, 64, P, 8, 8, P, 4, 65, 16, P, 4, None, 0, None, None, None, 0, 0.125, 0, P,
                                None), b"1 <= bl <= 64"),
     ("yapd_attn_paged_block", (P, P, 64, P, 8, 8, P, 4, 32, 6, P, 4, None, 0, None, None, None, 0, 0.125, 0, P,
@@ -217,6 +221,13 @@ def test_block_forward_checks_alignment_and_quant_layers_before_launching():
     layers[1].w_qkv = None  # unused by a quantised layer: the next rule is the one reported
     layers[1].q_down = kernels.T3QWeight(P + 4, P, P)
     assert call(model, ws) == EINVAL and b"q_down: packed weights must be 16-byte aligned" in lib.yapd_last_error()
+    # the dequantise-once scratch: one layer's four weights, 16-byte aligned
+    layers[1].q_down = kernels.T3QWeight(P, P, P)
+    need = 3 * 1024 * 1024 + 1024 * 1024 + 2 * 4096 * 1024 + 1024 * 4096
+    ws.wdq, ws.wdq_elems = P, need - 8
+    assert call(model, ws) == EINVAL and b"wdq must be 16-byte aligned and hold %d bf16" % need in lib.yapd_last_error()
+    ws.wdq, ws.wdq_elems = P + 4, need
+    assert call(model, ws) == EINVAL and b"wdq must be 16-byte aligned" in lib.yapd_last_error()
 
 
 def test_block_forward_rejects_incomplete_layer_and_head():

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import quant as Q
-from yapd_amd.quant import QuantLinear, qgemm_affine, quantize_affine
+from yapd_amd.quant import QuantLinear, dequant_affine, qgemm_affine, quantize_affine
 
 pytestmark = pytest.mark.gpu
 
@@ -73,3 +73,40 @@ def test_c5_projection_shapes_at_m8192(dev, bits, N, K):
     ref = a.float() @ w_hat.T
     rel = ((out.float() - ref).abs().max() / ref.abs().max()).item()
     assert rel <= 1e-2, rel
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("N,K", [(3072, 1024), (1000, 4096), (64, 64)])
+def test_dequant_affine_matches_the_oracle_bit_for_bit(dev, bits, N, K):
+    """``yapd_dequant_affine`` = bf16(fp32(scale * q + bias)): the codes unpacked by the oracle, the
+    product and sum exact in float64 and rounded once to fp32 (what the kernels' FMA does), then to
+    bf16.  Scales and biases of mixed sign and magnitude, so a dropped rounding or a mul-then-add
+    shows."""
+    g = torch.Generator().manual_seed(N + K + bits)
+    w = torch.randn(N, K, generator=g) * torch.logspace(-3, 0, K)[None, :] + torch.randn(N, 1, generator=g)
+    packed, s, b = quantize_affine(w.to(dev), bits)
+    out = dequant_affine(packed, s, b, bits)
+    q = Q.unpack(packed.cpu().numpy().view(np.uint32), bits, K).astype(np.float64)
+    s64 = np.repeat(s.cpu().numpy().astype(np.float64), 64, axis=1)
+    b64 = np.repeat(b.cpu().numpy().astype(np.float64), 64, axis=1)
+    ref = torch.from_numpy((s64 * q + b64).astype(np.float32)).bfloat16()
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+# C5's four shapes at M = 8192, and a partial last column tile at M = 16384
+@pytest.mark.parametrize("M,N,K", [(8192, 3072, 1024), (8192, 1024, 1024), (8192, 8192, 1024), (8192, 1024, 4096),
+                                   (16384, 1000, 1024)])
+def test_dequantise_once_route_equals_the_fused_kernel(dev, bits, M, N, K):
+    """With a scratch buffer and at least DEQUANT_MIN_ROWS rows, ``qgemm_affine`` dequantises W once and
+    runs the bf16 GEMM; the result equals the fused kernel's bit for bit (the same bf16 weights, the
+    same MFMA over K in the same order)."""
+    g = torch.Generator().manual_seed(M + N + K + bits)
+    w = torch.randn(N, K, generator=g) * 0.02
+    A = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    packed, s, b = quantize_affine(w.to(dev), bits)
+    scratch = torch.empty(N * K + 64, dtype=torch.bfloat16, device=dev)
+    fused = qgemm_affine(A, packed, s, b, bits)
+    once = qgemm_affine(A, packed, s, b, bits, scratch=scratch)
+    assert torch.equal(fused, once)
+    assert torch.equal(scratch[: N * K].view(N, K), dequant_affine(packed, s, b, bits))

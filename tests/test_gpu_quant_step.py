@@ -1,9 +1,11 @@
 """The quantised backbone: ``HipEngine(quant_bits=4 | 8)`` runs every layer
 projection on affine group-quantised weights in the MLX layout, as the
 reference's Metal engine does with ``CHATTERBOX_FLASH_MLX_QUANT_BITS``
-(chatterbox_flash/engines/mlx.py:171, 221-255).  The quantised kernels
-dequantise W once, ``w = bf16(fma(scale, q, bias))``, into the bf16 kernels'
-LDS layout and run their MFMA loop and epilogues, so:
+(chatterbox_flash/engines/mlx.py:171, 221-255).  Every route dequantises W as
+``w = bf16(fma(scale, q, bias))`` and runs the bf16 kernels' MFMA loop and
+epilogues on it -- the fused kernels tile by tile into LDS, the
+dequantise-once route (4096 rows or more, with the engine's scratch) into a
+bf16 copy of the layer's weights -- so:
 
   (i)  a quantised engine equals a bf16 engine built on the dequantised
        weights bit for bit -- the prefill's SOS hidden, and per graph replay of
@@ -55,11 +57,13 @@ def dequantize_model_(model, bits: int) -> None:
                 lin.weight.copy_(dequantized(lin.weight, bits))
 
 
-def build(dev, model, lens, bits, seed):
+def build(dev, model, lens, bits, seed, fused=False):
     pairs = len(lens)
     lps = lens + lens
     eng = HipEngine(model, max(lps) + 2 * BL, torch.bfloat16, batch_size=2 * pairs, page_table_seed=seed,
                     quant_bits=bits)
+    if fused:  # no dequantisation scratch: the fused quantised kernels at every row count
+        eng._wdq = None
     g = torch.Generator().manual_seed(seed + 1)
     prefixes = [torch.randn(lp, D, generator=g).to(torch.bfloat16) for lp in lens]
     sos = eng.prefix_forward([p.to(dev) for p in prefixes + prefixes])
@@ -82,18 +86,20 @@ def replay(w):
     return eng._buffers(rows, BL).hidden.view(rows, BL, -1).clone(), eng._g_logits.clone(), out, res
 
 
-# 256 pairs (16384 rows per projection): every quantised projection on 256 x 256
-# direct-load tiles; 64 pairs (4096): QKV on register-staged 128 x 128 tiles, o and
-# down on direct-load 128 x 128 tiles (one per CU), gate/up on 256 x 256 tiles;
-# 16 pairs (1024): QKV, o and down on direct-load 128 x 128 tiles, gate/up
-# register-staged.  The prefill's packed steps add other sizes.
-@pytest.mark.parametrize("bits,pairs", [(4, 256), (8, 256), (4, 64), (8, 16)])
-def test_quantised_engine_equals_bf16_engine_on_dequantised_weights(dev, bits, pairs):
+# At 4096 rows or more (64 and 256 pairs, and the prefill's packed steps of
+# 16384 tokens) the engine dequantises each layer's weights once into its
+# scratch and runs the bf16 kernels; with fused=True (no scratch) and at 16
+# pairs (1024 rows) the fused kernels run: at 256 pairs every projection on
+# 256 x 256 direct-load tiles; at 16 pairs QKV, o and down on direct-load
+# 128 x 128 tiles and gate/up register-staged.
+@pytest.mark.parametrize("bits,pairs,fused", [(4, 256, False), (8, 256, False), (4, 64, False), (8, 16, False),
+                                              (4, 256, True), (8, 64, True)])
+def test_quantised_engine_equals_bf16_engine_on_dequantised_weights(dev, bits, pairs, fused):
     lens = uniform_lengths(pairs, 150, 600, seed=61)
     model_q = make_t3(n_layers=4, seed=60, norm_jitter=True, learned_pos_emb=True, device=dev)
     model_e = make_t3(n_layers=4, seed=60, norm_jitter=True, learned_pos_emb=True, device=dev)
     dequantize_model_(model_e, bits)
-    wq = build(dev, model_q, lens, bits, seed=62)
+    wq = build(dev, model_q, lens, bits, seed=62, fused=fused)
     we = build(dev, model_e, lens, 0, seed=62)
     assert wq["eng"].quant_bits == bits and we["eng"].quant_bits == 0
     assert torch.equal(wq["sos"], we["sos"])

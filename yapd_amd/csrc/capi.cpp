@@ -27,4 +27,4 @@ int check_hip(hipError_t e, const char* what) {
 
 extern "C" const char* yapd_last_error(void) { return yapd::g_last_error; }
 
-extern "C" int yapd_abi_version(void) { return 3; }
+extern "C" int yapd_abi_version(void) { return 4; }

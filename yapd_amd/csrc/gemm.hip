@@ -1917,6 +1917,75 @@ int qgemm_qkv_rope_kv(const void* A, int64_t lda, const QWeight& w, int M, int K
   return launch_q<kEpiQkv>(p, w.bits, stream);
 }
 
+namespace {
+// Dequantisation of up to four weights in one launch: each thread turns the
+// 8 codes of one 16-byte output chunk into bf16(scale * q + bias) with the
+// arithmetic of the fused kernels' W loader (dq_pair), so a GEMM on the
+// result equals the fused quantised GEMM bit for bit.
+struct DqJob {
+  const uint32_t* packed;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  uint16_t* out;       // bf16 [N, K], row pitch K
+  int N, K;
+  int64_t chunk0;      // first 16-byte output chunk of this job in the launch
+};
+struct DqParams {
+  DqJob job[kMaxDqJobs];
+  int n_jobs;
+  int64_t chunks;      // all jobs' chunks
+};
+
+template <int BITS>
+__global__ __launch_bounds__(256) void dequant_affine_kernel(const DqParams p) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= p.chunks) return;
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxDqJobs; ++i)
+    if (i < p.n_jobs && t >= p.job[i].chunk0) j = i;
+  const DqJob& q = p.job[j];
+  const int64_t c = t - q.chunk0;
+  const int cpr = q.K / 8;  // chunks per row
+  const int n = static_cast<int>(c / cpr), k0 = static_cast<int>(c % cpr) * 8;
+  const float sc = f16_to_f32(q.scales[static_cast<int64_t>(n) * (q.K / 64) + k0 / 64]);
+  const float bi = f16_to_f32(q.biases[static_cast<int64_t>(n) * (q.K / 64) + k0 / 64]);
+  const uint32_t* row = q.packed + static_cast<int64_t>(n) * (q.K * BITS / 32);
+  u32x4_t v;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int first = k0 + 2 * h;  // code index in the row
+    v[h] = dq_pair<BITS>(row[first * BITS / 32], (first * BITS) % 32, sc, bi);
+  }
+  *reinterpret_cast<u32x4_t*>(q.out + static_cast<int64_t>(n) * q.K + k0) = v;
+}
+}  // namespace
+
+int dequant_affine(const QWeight* w, const int* N, const int* K, uint16_t* const* out, int n, hipStream_t stream) {
+  YAPD_REQUIRE(n >= 1 && n <= kMaxDqJobs, "dequant_affine: 1 to %d weights per launch (got %d)", kMaxDqJobs, n);
+  DqParams p{};
+  int64_t chunks = 0;
+  for (int i = 0; i < n; ++i) {
+    if (int rc = qweight_checks(w[i], N[i], K[i], "dequant_affine")) return rc;
+    YAPD_REQUIRE(w[i].bits == w[0].bits, "dequant_affine: one bit width per launch");
+    YAPD_REQUIRE(out[i] && (reinterpret_cast<uintptr_t>(out[i]) & 15u) == 0,
+                 "dequant_affine: outputs must be non-NULL and 16-byte aligned");
+    p.job[i] = DqJob{w[i].packed, w[i].scales, w[i].biases, out[i], N[i], K[i], chunks};
+    chunks += static_cast<int64_t>(N[i]) * K[i] / 8;
+  }
+  p.n_jobs = n;
+  p.chunks = chunks;
+  const int64_t blocks = (chunks + 255) / 256;
+  YAPD_REQUIRE(blocks <= INT32_MAX, "dequant_affine: weights too large");
+  if (w[0].bits == 4) {
+    hipLaunchKernelGGL(dequant_affine_kernel<4>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(dequant_affine_kernel<8>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
+  }
+  YAPD_LAUNCH_CHECK("dequant_affine_kernel launch");
+  return YAPD_OK;
+}
+
 }  // namespace yapd
 
 extern "C" int yapd_gemm_qkv_rope_kv(const void* A, int64_t lda, const void* W_qkv, int M, int K, int n_heads,
@@ -1975,4 +2044,12 @@ extern "C" int yapd_qgemm_affine(const void* A, int64_t lda, const uint32_t* w_p
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return bits == 4 ? yapd::launch_gemm<yapd::kEpiStore, yapd::kAPlain, 4>(p, st)
                    : yapd::launch_gemm<yapd::kEpiStore, yapd::kAPlain, 8>(p, st);
+}
+
+extern "C" int yapd_dequant_affine(const uint32_t* w_packed, const void* scales, const void* biases, int bits,
+                                   int group_size, int N, int K, void* W_out, void* stream) {
+  YAPD_REQUIRE(group_size == 64, "dequant_affine: group_size must be 64 (got %d)", group_size);
+  const yapd::QWeight w{w_packed, static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases), bits};
+  uint16_t* out = static_cast<uint16_t*>(W_out);
+  return yapd::dequant_affine(&w, &N, &K, &out, 1, static_cast<hipStream_t>(stream));
 }

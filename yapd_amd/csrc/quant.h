@@ -40,4 +40,10 @@ int qgemm_qkv_rope_kv(const void* A, int64_t lda, const QWeight& w_qkv, int M, i
                       const int32_t* tok_row, void* q_out, void* kv_pool, int64_t n_pages, const int32_t* page_table,
                       int table_stride, int table_cols, hipStream_t stream);
 
+// bf16(scale * q + bias) of n <= kMaxDqJobs weights (one bit width) into
+// out[i] [N[i], K[i]] (row pitch K[i], 16-byte aligned), in one launch: the
+// weights the fused kernels dequantise on their way into LDS, bit for bit.
+constexpr int kMaxDqJobs = 4;
+int dequant_affine(const QWeight* w, const int* N, const int* K, uint16_t* const* out, int n, hipStream_t stream);
+
 }  // namespace yapd

@@ -31,6 +31,20 @@ struct PackedRows {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Quantised layers at this many rows or more, given the workspace's wdq
+// buffer, dequantise their four weights once into it and run the bf16
+// kernels: the fused kernels redo the dequantisation for every row tile,
+// while here it is one pass over the weights per layer.  Below, the fused
+// kernels read the 4- or 8-bit codes themselves (a quarter or half of the
+// bf16 bytes), which is what pays at few rows.
+constexpr int kDequantMinRows = 4096;
+
+// bf16 elements of one layer's dequantised projections: qkv, o, gate/up, down.
+int64_t layer_weight_elems(int D, int HD, int F) {
+  return static_cast<int64_t>(3 * HD) * D + static_cast<int64_t>(D) * HD + static_cast<int64_t>(2 * F) * D +
+         static_cast<int64_t>(D) * F;
+}
+
 yapd::QWeight qw(const yapd_t3_qweight& w, int bits) {
   return yapd::QWeight{w.packed, static_cast<const uint16_t*>(w.scales), static_cast<const uint16_t*>(w.biases),
                        bits};
@@ -70,6 +84,9 @@ int model_checks(const yapd_t3_model* m, const yapd_t3_workspace* ws, int rows, 
       YAPD_REQUIRE(al16(L.w_qkv) && al16(L.w_o) && al16(L.w_gate_up) && al16(L.w_down),
                    "t3_block_forward: layer %d weights must be 16-byte aligned", li);
     } else {
+      YAPD_REQUIRE(!ws->wdq || (al16(ws->wdq) && ws->wdq_elems >= layer_weight_elems(D, HD, F)),
+                   "t3_block_forward: wdq must be 16-byte aligned and hold %lld bf16 (got %lld)",
+                   static_cast<long long>(layer_weight_elems(D, HD, F)), static_cast<long long>(ws->wdq_elems));
       YAPD_TRY(yapd::qweight_checks(qw(L.q_qkv, L.qbits), 3 * HD, D, "t3_block_forward q_qkv"));
       YAPD_TRY(yapd::qweight_checks(qw(L.q_o, L.qbits), D, HD, "t3_block_forward q_o"));
       YAPD_TRY(yapd::qweight_checks(qw(L.q_gate_up, L.qbits), 2 * F, D, "t3_block_forward q_gate_up"));
@@ -98,7 +115,29 @@ int run_layers(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* 
   const hipStream_t hst = static_cast<hipStream_t>(st);
   for (int li = 0; li < m->n_layers; ++li) {
     const yapd_t3_layer& L = m->layers[li];
-    const bool q = L.qbits != 0;
+    // q: the fused quantised kernels; with dq the weights are dequantised
+    // into wdq first and the bf16 kernels run on them
+    const bool dq = L.qbits != 0 && ws->wdq != nullptr && M >= kDequantMinRows;
+    const bool q = L.qbits != 0 && !dq;
+    const void* w_qkv = L.w_qkv;
+    const void* w_o = L.w_o;
+    const void* w_gate_up = L.w_gate_up;
+    const void* w_down = L.w_down;
+    if (dq) {
+      uint16_t* out[4];
+      out[0] = static_cast<uint16_t*>(ws->wdq);
+      out[1] = out[0] + static_cast<int64_t>(3 * HD) * D;
+      out[2] = out[1] + static_cast<int64_t>(D) * HD;
+      out[3] = out[2] + static_cast<int64_t>(2 * F) * D;
+      const yapd::QWeight w[4] = {qw(L.q_qkv, L.qbits), qw(L.q_o, L.qbits), qw(L.q_gate_up, L.qbits),
+                                  qw(L.q_down, L.qbits)};
+      const int N[4] = {3 * HD, D, 2 * F, D}, K[4] = {D, HD, D, F};
+      YAPD_TRY(yapd::dequant_affine(w, N, K, out, 4, hst));
+      w_qkv = out[0];
+      w_o = out[1];
+      w_gate_up = out[2];
+      w_down = out[3];
+    }
     if (q) {
       YAPD_TRY(yapd::qgemm_qkv_rope_kv(xn, D, qw(L.q_qkv, L.qbits), M, D, H, m->rope_cos, m->rope_sin,
                                        m->rope_positions, pos0, bl, rows, pk ? pk->row_start : nullptr,
@@ -107,7 +146,7 @@ int run_layers(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* 
     }
     if (pk == nullptr) {
       if (!q)
-        YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0,
+        YAPD_TRY(yapd_gemm_qkv_rope_kv(xn, D, w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions, pos0,
                                        bl, ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride,
                                        m->table_cols, st));
       YAPD_TRY(yapd_attn_paged_block(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols,
@@ -115,7 +154,7 @@ int run_layers(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* 
                                      ws->part_o, ws->part_ml, ws->n_slots, scale, causal, ws->attn, st));
     } else {
       if (!q)
-        YAPD_TRY(yapd::gemm_qkv_rope_kv_packed(xn, D, L.w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions,
+        YAPD_TRY(yapd::gemm_qkv_rope_kv_packed(xn, D, w_qkv, M, D, H, m->rope_cos, m->rope_sin, m->rope_positions,
                                                pos0, rows, pk->row_start, pk->tok_row, ws->q, L.kv_pool, m->n_pages,
                                                m->page_table, m->table_stride, m->table_cols, hst));
       YAPD_TRY(yapd::attn_launch(ws->q, L.kv_pool, m->n_pages, m->page_table, m->table_stride, m->table_cols, kv_len,
@@ -125,15 +164,15 @@ int run_layers(const yapd_t3_model* m, const yapd_t3_workspace* ws, const void* 
     if (q) {
       YAPD_TRY(yapd::qgemm_residual(ws->attn, HD, qw(L.q_o, L.qbits), M, D, HD, res, D, hst));
     } else {
-      YAPD_TRY(yapd_gemm_bf16_residual(ws->attn, HD, L.w_o, HD, M, D, HD, res, D, st));
+      YAPD_TRY(yapd_gemm_bf16_residual(ws->attn, HD, w_o, HD, M, D, HD, res, D, st));
     }
     YAPD_TRY(yapd_rmsnorm(nullptr, nullptr, res, L.ln_post, L.eps_post, M, D, xn, st));
     if (q) {
       YAPD_TRY(yapd::qgemm_swiglu(xn, D, qw(L.q_gate_up, L.qbits), M, F, D, ws->act, F, hst));
       YAPD_TRY(yapd::qgemm_residual(ws->act, F, qw(L.q_down, L.qbits), M, D, F, res, D, hst));
     } else {
-      YAPD_TRY(yapd_gemm_swiglu(xn, D, L.w_gate_up, M, F, D, ws->act, F, st));
-      YAPD_TRY(yapd_gemm_bf16_residual(ws->act, F, L.w_down, F, M, D, F, res, D, st));
+      YAPD_TRY(yapd_gemm_swiglu(xn, D, w_gate_up, M, F, D, ws->act, F, st));
+      YAPD_TRY(yapd_gemm_bf16_residual(ws->act, F, w_down, F, M, D, F, res, D, st));
     }
     const bool last = li + 1 == m->n_layers;
     const void* wn = last ? m->final_norm : m->layers[li + 1].ln_in;

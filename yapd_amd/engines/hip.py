@@ -141,15 +141,19 @@ class HipEngine:
             self._final_norm = tf.norm.weight.to(dtype).contiguous()
             self._final_eps = float(tf.norm.variance_epsilon)
             self._ffn = self._w[0]["wd"].shape[1]
+            self._wdq: Optional[Tensor] = None
             if self._quant_bits:
                 # Quantise the fused copies row by row (groups of 64 along the input dim,
                 # so fusing and interleaving rows commutes with quantising); the bf16
-                # copies are dropped.
+                # copies are dropped.  One layer's dequantised weights (bf16) are the
+                # scratch of the dequantise-once route the native step takes at many rows.
                 from ..quant import quantize_affine
                 for w in self._w:
                     for key in ("wqkv", "wo", "wgu", "wd"):
                         w["q_" + key] = quantize_affine(w[key], self._quant_bits)
                         w[key] = None
+                F = self._ffn
+                self._wdq = torch.empty(3 * H * 64 * D + D * H * 64 + 2 * F * D + D * F, dtype=dtype, device=dev)
             # RoPE table from the model's own rotary embedding (handles llama3
             # scaling; engines/flashinfer.py:195-255), values of the model dtype.
             dummy = torch.zeros(1, 1, D, device=dev, dtype=dtype)
@@ -294,7 +298,7 @@ class HipEngine:
             buf.delta.data_ptr(), buf.act.data_ptr(), plan.work.data_ptr(), int(plan.work.shape[0]),
             kernels.ptr(plan.merge), n_merge,
             kernels.ptr(getattr(plan, "counts", None)), kernels.ptr(plan.part_o), kernels.ptr(plan.part_ml),
-            int(plan.n_slots))
+            int(plan.n_slots), kernels.ptr(self._wdq), 0 if self._wdq is None else self._wdq.numel())
 
     def _descriptor(self, row0: int, table: Optional[Tensor] = None) -> "kernels.T3Model":
         """The native model descriptor whose batch row 0 is page-table row ``row0``, or whose

@@ -55,6 +55,7 @@ _SIGNATURES = {
                                               c_int, c_void]),
     "yapd_qgemm_affine": (c_int, [c_void, c_i64, c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_int,
                                   c_void, c_i64, c_void]),
+    "yapd_dequant_affine": (c_int, [c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_void, c_void]),
     "yapd_mfma_peak_probe": (c_int, [c_int, c_int, c_int, c_void, c_void]),
     "yapd_hbm_read_probe": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
     "yapd_tick_update": (c_int, [c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_void, c_i64,
@@ -104,7 +105,8 @@ class T3Workspace(ctypes.Structure):
     """``yapd_t3_workspace`` of include/yapd_t3.h."""
     _fields_ = [("residual", c_void), ("q", c_void), ("attn", c_void), ("normed", c_void), ("delta", c_void),
                 ("act", c_void), ("work", c_void), ("n_work", c_int), ("merge", c_void), ("n_merge", c_int),
-                ("counts", c_void), ("part_o", c_void), ("part_ml", c_void), ("n_slots", c_int)]
+                ("counts", c_void), ("part_o", c_void), ("part_ml", c_void), ("n_slots", c_int),
+                ("wdq", c_void), ("wdq_elems", c_i64)]
 
 
 class HipKernelError(RuntimeError):
