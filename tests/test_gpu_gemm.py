@@ -45,9 +45,10 @@ def test_gemm_bf16(dev, M, N, K):
 
 
 # (16384, 1000, 1024): persistent kernel, one round in XCD bands, a partial last column tile;
-# (32768, 1024, 1024): persistent kernel, two rounds in row-major order
+# (32768, 1024, 1024): persistent kernel, two rounds in row-major order; (16484, 1024, 1024): the
+# same with 65 row tiles (no bands) and a partial last row tile
 @pytest.mark.parametrize("M,N,K", [(200, 1024, 1024), (16384 // 8, 1024, 4096), (4100, 1024, 1024),
-                                   (16384, 1000, 1024), (32768, 1024, 1024)])
+                                   (16384, 1000, 1024), (32768, 1024, 1024), (16484, 1024, 1024)])
 def test_gemm_residual_equals_separate_add(dev, M, N, K):
     """The fused residual add is bit-identical to the projection stored in bf16
     followed by the bf16 residual add (HF's two roundings)."""
