@@ -110,10 +110,13 @@ def test_gemm_head_shift(dev, rows):
 # straddle the q/k boundary (q = columns [0, 384)) and one tile holds only V
 # columns (no RoPE rows staged); 2 heads: q, k and v inside one small tile.
 # 512 x 32 rows (the step's shape) and 515 x 32: the persistent kernel, in XCD
-# row bands and, with 65 row tiles (the last one partial), row-major.
-@pytest.mark.parametrize("rows,H", [(3, 16), (180, 16), (320, 6), (3, 2), (512, 16), (515, 16)])
-def test_gemm_qkv_rope_kv(dev, rows, H):
-    D, bl = 1024, 32
+# row bands and, with 65 row tiles (the last one partial), row-major; also at
+# blocks of 16 (704 x 16 rows: 44 row tiles, row-major) and 64 (256 x 64
+# rows), whose blocks start at any slot of a page like the others.
+@pytest.mark.parametrize("rows,H,bl", [(3, 16, 32), (180, 16, 32), (320, 6, 32), (3, 2, 32), (512, 16, 32),
+                                       (515, 16, 32), (704, 16, 16), (256, 16, 64)])
+def test_gemm_qkv_rope_kv(dev, rows, H, bl):
+    D = 1024
     M = rows * bl
     A = rnd(M, D, seed=11)
     Wqkv = rnd(3 * H * 64, D, std=0.02, seed=12)
